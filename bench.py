@@ -1,0 +1,222 @@
+"""Benchmark of the verify/decode paged-attention layer call on one MI355X.
+
+A step is one layer call of verify attention (Qwen3-8B shape, B=16,
+q_len=5, contexts U[256, 4096], 24,576-block pool, fp16) on inputs already
+resident in HBM.  Steps cycle ``cur_layer`` over all 36 layers so the
+~144 MB per-layer working set cannot stay in the 256 MB Infinity Cache.
+The timed steps are replayed from a HIP graph of one pass over the layers
+(no host launch overhead inside the timed region).  A secondary line
+measures Draft decode (Qwen3-0.6B shape, B=64).  The CPU baseline times the
+numpy oracle on the same inputs on this host's cores.
+
+Prints one JSON line (see ``--help``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=720, help="timed layer calls (multiple of the layer count)")
+    p.add_argument("--warmup", type=int, default=72)
+    p.add_argument("--workload", default="target_verify")
+    p.add_argument("--secondary", default="draft_decode", help="second workload ('' to skip)")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
+                   help="bound on CPU oracle time (0 disables the CPU baseline)")
+    return p.parse_args()
+
+
+def measure(name: str, seed: int, steps: int, warmup: int):
+    """Time `steps` layer calls of workload `name`; returns (result dict, workload)."""
+    import torch
+
+    from nebulasd_amd.config import EngineConfig, ModelConfig
+    from nebulasd_amd.infer_state import build_infer_state, rope_cache
+    from nebulasd_amd.kernels import paged_attention
+    from nebulasd_amd.workload import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(name, seed, device=dev)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    cos, sin = rope_cache(128, mc.rope_theta, max(w.seq_lens) + 1, dev)
+    st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, dev)
+    L = mc.num_layers
+    o = torch.empty_like(w.q)
+
+    def one_pass():
+        for layer in range(L):
+            paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o)
+
+    one_pass()  # builds the plan, sets kernel attributes
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            one_pass()
+    torch.cuda.synchronize()
+    reps = max(1, steps // L)
+    wreps = max(1, warmup // L)
+    for _ in range(wreps):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n = reps * L
+    us = start.elapsed_time(end) * 1e3 / n
+    nbytes = w.algorithmic_bytes()
+    gbps = nbytes / (us * 1e-6) / 1e9
+    plan = st.attn_plan
+    res = {
+        "workload": name,
+        "steps": n,
+        "us_per_layer_call": us,
+        "wall_ms": wall * 1e3,
+        "algorithmic_bytes": nbytes,
+        "hbm_gbps": gbps,
+        "hbm_frac": gbps / HBM_PEAK_GBPS,
+        "tokens_per_s": w.rows / (us * 1e-6 * L),
+        "tflops": w.flops() / (us * 1e-6) / 1e12,
+        "rows": w.rows,
+        "kv_tokens": w.kv_tokens(),
+        "plan_workers": int(plan.host[5]),
+        "plan_rows_max": plan.rows_max,
+    }
+    del graph
+    return res, w
+
+
+def cpu_baseline(w, budget_s: float):
+    """Time the numpy oracle (fp32) on the same inputs; bounded to ~budget_s seconds."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    import oracle
+
+    layer = w.spec.num_layers // 2
+    bs = 16
+    bt = w.block_table.cpu().numpy()
+    ids = sorted({int(bt[s, i]) for s, n in zip(w.seq_ids, w.seq_lens) for i in range((n + bs - 1) // bs)})
+    remap = np.zeros(w.k_cache.shape[0], dtype=np.int64)
+    remap[ids] = np.arange(len(ids))
+    idx = torch.tensor(ids, device=w.k_cache.device)
+    kc = w.k_cache[idx, layer].unsqueeze(1).cpu().numpy()
+    vc = w.v_cache[idx, layer].unsqueeze(1).cpu().numpy()
+    bt_s = remap[bt]
+    q = w.q.cpu().numpy()
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    times = []
+    with threadpool_limits(limits=cores):
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        t_end = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            oracle.paged_attention(q, kc, vc, bt_s, w.seq_ids, w.seq_lens, 0, dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end or len(times) >= 20:
+                break
+    us = float(np.median(times)) * 1e6
+    return {
+        "value": us,
+        "unit": "us/layer-call",
+        "cores": int(min(threads, cores)),
+        "kind": "port",
+        "sample": f"{len(times)} layer calls of {w.spec.name} (one layer, same seeded inputs), "
+                  f"numpy fp32 oracle, median",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(every box has a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from nebulasd_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from nebulasd_amd.build import build
+
+        build()
+    res, w = measure(args.workload, args.seed, args.steps, args.warmup)
+    print(f"# {args.workload}: {res['us_per_layer_call']:.2f} us/layer-call, "
+          f"{res['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        cpu = cpu_baseline(w, args.cpu_baseline_seconds)
+    spec = w.spec
+    del w
+    torch.cuda.empty_cache()
+    secondary = None
+    if args.secondary:
+        secondary, w2 = measure(args.secondary, args.seed, args.steps, args.warmup)
+        del w2
+        torch.cuda.empty_cache()
+    line = {
+        "metric": "verify/decode attn µs per layer + HBM GB/s (% peak), Qwen3-8B B=16 q_len=5",
+        "value": res["us_per_layer_call"],
+        "unit": "us/layer-call",
+        "n_gpus": 1,
+        "steps": res["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": res["us_per_layer_call"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: Qwen3-8B attention shape (32q/8kv heads, d=128), B={spec.batch}, "
+                        f"q_len={spec.q_len}, contexts {spec.ctx[0]} [{spec.ctx[1]},{spec.ctx[2]}], "
+                        f"block 16, pool {spec.pool_blocks} blocks, layers cycled 0..{spec.num_layers - 1}",
+            "batch": spec.batch,
+            "q_len": spec.q_len,
+            "seed": args.seed,
+        },
+        "hbm_gbps": res["hbm_gbps"],
+        "hbm_frac": res["hbm_frac"],
+        "tokens_per_s": res["tokens_per_s"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": res["hbm_gbps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": res["hbm_frac"],
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "detail": res,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/*
+ * nsd_attn.h -- C ABI of the MI355X (gfx950) verify/decode paged-attention
+ * path of NebulaSD's swiftLLM backend.
+ *
+ * All tensors are caller-owned device buffers passed as raw pointers with
+ * int64 sizes.  Every entry point is stream-ordered on the caller's
+ * hipStream_t (passed as void*), never synchronises the host, never
+ * allocates device memory, and returns an int status (NSD_OK == 0).  On a
+ * nonzero status nsd_last_error() returns a thread-local message.
+ *
+ * Fixed layouts (identical to the reference, byte for byte):
+ *   k_cache, v_cache : fp16 [num_blocks, num_layers, num_kv_heads, block_size, head_dim]
+ *                      (swiftLLM/swiftllm/worker/model.py:152-166)
+ *   block_table      : int32 [bt_rows, bt_stride] (row = seq_id)
+ *                      (swiftLLM/swiftllm/worker/block_manager.py:112-117)
+ *   q, o             : fp16 [n_rows, num_q_heads, head_dim], contiguous
+ *   k, v (new rows)  : fp16 [n_rows, num_kv_heads, head_dim], contiguous
+ * Supported: head_dim == 128, block_size == 16, num_q_heads % num_kv_heads == 0.
+ *
+ * `status` arguments are optional (may be NULL) device int32 words: a kernel
+ * that meets an out-of-range block id, seq_id or position skips that access
+ * and ORs a flag into *status (NSD_STATUS_*), so bad metadata never faults.
+ */
+#ifndef NSD_ATTN_H
+#define NSD_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSD_OK 0
+#define NSD_ERR_INVALID 1      /* bad argument (null pointer, size, range) */
+#define NSD_ERR_UNSUPPORTED 2  /* shape outside the supported set */
+#define NSD_ERR_HIP 3          /* HIP runtime error */
+#define NSD_ERR_WORKSPACE 4    /* workspace / plan buffer too small */
+
+#define NSD_STATUS_BAD_BLOCK 1     /* block id outside [0, num_blocks) */
+#define NSD_STATUS_BAD_SEQ 2       /* seq_id outside [0, bt_rows) or position outside the row */
+#define NSD_STATUS_BAD_POSITION 4  /* RoPE position outside the cos/sin table */
+
+#define NSD_PLAN_HEADER_WORDS 16
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nsd_version(void);
+
+/* Thread-local message of the last failing call on this thread. */
+const char* nsd_last_error(void);
+
+/*
+ * QK-RMSNorm building block.  Replaces rmsnorm_inplace
+ * (swiftLLM/swiftllm/worker/kernels/rmsnorm.py:26-37, kernel :5-24):
+ * per row of `hidden` fp16 values, y = fp16(x * 1/sqrt(mean(x^2)+eps) * w),
+ * computed in fp32, in place.
+ */
+int nsd_rmsnorm_inplace(void* x, const void* w, int64_t n_rows, int64_t hidden,
+                        float eps, void* stream);
+
+/*
+ * Rotate-half RoPE, in place on q [n_tokens, Hq, d] and k [n_tokens, Hkv, d]
+ * from per-token tables cos/sin [n_tokens, d/2] fp16.  Replaces
+ * rotary_embedding_inplace (swiftLLM/swiftllm/worker/kernels/rotary_emb.py:44-58,
+ * kernel :7-42).  Arithmetic in fp32, one rounding to fp16.
+ */
+int nsd_rotary_embedding_inplace(void* q, void* k, const void* cos_table,
+                                 const void* sin_table, int64_t n_tokens,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 void* stream);
+
+/*
+ * Decode/verify KV store.  Replaces the decoding half of store_kvcache
+ * (swiftLLM/swiftllm/worker/kernels/kvcache_mgmt.py:81-122, kernel :50-79):
+ * row r copies k[r], v[r] ([Hkv, d]) to slot (seq_lens[r]-1) % block_size of
+ * block block_table[seq_ids[r], (seq_lens[r]-1) / block_size] at `layer`.
+ * seq_ids / seq_lens are device int32 [n_rows].  Bit-exact copy.
+ */
+int nsd_store_kvcache(const void* k, const void* v, void* k_cache, void* v_cache,
+                      const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
+                      const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                      int64_t num_blocks, int num_layers, int layer, int num_kv_heads,
+                      int head_dim, int block_size, int32_t* status, void* stream);
+
+/*
+ * Prefill KV store.  Replaces the prefill half of store_kvcache
+ * (swiftLLM/swiftllm/worker/kernels/kvcache_mgmt.py:10-48): sequence s copies
+ * its tokens k/v[start_locs[s] + i] to position i (0 <= i < prefill_lens[s])
+ * of block_table[seq_ids[s]].  All index arrays are device int32 [n_seqs].
+ */
+int nsd_store_kvcache_prefill(const void* k, const void* v, void* k_cache, void* v_cache,
+                              const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
+                              const int32_t* seq_ids, const int32_t* start_locs,
+                              const int32_t* prefill_lens, int64_t n_seqs,
+                              int64_t max_prefill_len, int64_t num_blocks, int num_layers,
+                              int layer, int num_kv_heads, int head_dim, int block_size,
+                              int32_t* status, void* stream);
+
+/*
+ * Fused attention prologue of one decode/verify layer call, one launch.
+ * Replaces the sequence rmsnorm_inplace(q) -> rmsnorm_inplace(k) ->
+ * rotary_embedding_inplace -> store_kvcache of
+ * swiftLLM/swiftllm/worker/layers/transformer_layer.py:114-145:
+ *   q[r,h] = rope(fp16(rmsnorm(q[r,h]) * q_norm_w))    (in place)
+ *   k[r,h] = rope(fp16(rmsnorm(k[r,h]) * k_norm_w))    (in place)
+ *   k_cache/v_cache slot of (seq_ids[r], seq_lens[r]-1) <- k[r], v[r]
+ * RoPE position = seq_lens[r]-1 (model.py:343-354), looked up in the full
+ * cos/sin caches [n_positions, d/2] fp16 (model.py:242-252).
+ * q_norm_w / k_norm_w may be NULL to skip the norm (models without QK-norm).
+ */
+int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w,
+                           const void* k_norm_w, float eps, const void* cos_cache,
+                           const void* sin_cache, int64_t n_positions, void* k_cache,
+                           void* v_cache, const int32_t* block_table, int64_t bt_rows,
+                           int64_t bt_stride, const int32_t* seq_ids, const int32_t* seq_lens,
+                           int64_t n_rows, int64_t num_blocks, int num_layers, int layer,
+                           int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                           int32_t* status, void* stream);
+
+/*
+ * Attention work plan (host side, no HIP calls).  The reference picks a
+ * split size per forward (swiftLLM/swiftllm/worker/model.py:365-384) and
+ * launches one program per (row, q-head, split) (kernels/paged_attn.py:182-211).
+ * Here the plan is built once per forward from the host copies of the
+ * rows' seq_ids / seq_lens (the lists model.forward already holds,
+ * model.py:304-341) and reused by every layer:
+ *   - consecutive rows with equal seq_id and seq_len increasing by one form
+ *     a verify group (rows of speculative.py:75-89); each group is attended
+ *     once per KV head with GQA-group x q_len query rows packed together;
+ *     max_group_rows = 1 keeps every row its own group;
+ *   - the (group, kv head, 32-token chunk) work is cut into n_workers equal
+ *     contiguous ranges; a group/head cut across ranges gets fp32 partials
+ *     (normalised O and log2-sum-exp) merged by a combine pass.
+ * nsd_attn_plan_bound gives an upper bound on the plan size in int32 words.
+ * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
+ * 0 <= seq_id < bt_rows), writes the plan into `plan` (capacity
+ * `plan_capacity` words), and returns its size and the workspace bytes
+ * nsd_paged_attention needs.
+ */
+int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_workers);
+int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                        int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                        int64_t bt_rows, int64_t bt_stride, int n_workers,
+                        int max_group_rows, int32_t* plan, int64_t plan_capacity,
+                        int64_t* plan_words, int64_t* workspace_bytes);
+
+/*
+ * Number of workers (workgroups) that fill the current device for a plan
+ * whose groups hold at most `max_rows` query rows per KV head (occupancy x
+ * compute units).  Needs a GPU.
+ */
+int nsd_attn_num_workers(int max_rows, int* n_workers);
+
+/*
+ * Paged verify/decode attention for one layer.  Replaces paged_attention
+ * (swiftLLM/swiftllm/worker/kernels/paged_attn.py:152-222, kernels :9-149):
+ * row r, q-head qh attends tokens [0, seq_len[r]) of block_table[seq_id[r]]
+ * in kv head qh / (Hq/Hkv) with scores q.k * softmax_scale; o[r, qh] is the
+ * softmax-weighted sum of V (fp16 out, fp32 math).  If lse != NULL it also
+ * writes ln(sum exp(score)) as fp32 [n_rows, Hq].
+ * plan_host / plan_dev: the same plan words on the host and on the device.
+ * workspace: device buffer of at least the bytes reported by the plan.
+ */
+int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
+                        const void* v_cache, int64_t num_blocks, int num_layers, int layer,
+                        int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                        const int32_t* block_table, int64_t bt_stride,
+                        const int32_t* plan_host, const int32_t* plan_dev,
+                        void* workspace, int64_t workspace_bytes, float softmax_scale,
+                        int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSD_ATTN_H */

@@ -1,0 +1,179 @@
+// Host-only part of the C ABI: error plumbing, version, and the attention
+// work planner (no HIP calls, so it also runs on machines without a GPU).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "nsd_common.h"
+
+namespace nsd {
+
+namespace {
+thread_local std::string g_last_error;
+constexpr int64_t kMinChunksPerWorker = 4;  // one 32-token chunk per wave of a workgroup
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+}  // namespace nsd
+
+using namespace nsd;
+
+extern "C" int nsd_version(void) { return 100; }
+
+extern "C" const char* nsd_last_error(void) { return g_last_error.c_str(); }
+
+static int64_t round_up8(int64_t x) { return (x + 7) / 8 * 8; }
+
+extern "C" int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_workers) {
+  if (n_rows < 0 || num_kv_heads <= 0 || n_workers <= 0) return -1;
+  const int64_t segs = n_rows * num_kv_heads;
+  const int64_t nw = round_up8(n_workers);
+  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + (nw + 1) + 4 * (nw + segs) + 4 * segs;
+}
+
+extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                                   int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int64_t bt_rows, int64_t bt_stride, int n_workers,
+                                   int max_group_rows, int32_t* plan, int64_t plan_capacity,
+                                   int64_t* plan_words, int64_t* workspace_bytes) {
+  if (n_rows < 0) return fail(NSD_ERR_INVALID, "plan: n_rows=%lld < 0", (long long)n_rows);
+  if (n_rows > 0 && (seq_ids == nullptr || seq_lens == nullptr))
+    return fail(NSD_ERR_INVALID, "plan: null seq_ids/seq_lens");
+  if (plan == nullptr || plan_words == nullptr || workspace_bytes == nullptr)
+    return fail(NSD_ERR_INVALID, "plan: null output pointer");
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(NSD_ERR_INVALID, "plan: num_q_heads=%d not a multiple of num_kv_heads=%d",
+                num_q_heads, num_kv_heads);
+  if (head_dim != kHeadDim) return fail(NSD_ERR_UNSUPPORTED, "plan: head_dim=%d (only 128)", head_dim);
+  if (block_size != kBlockTokens)
+    return fail(NSD_ERR_UNSUPPORTED, "plan: block_size=%d (only 16)", block_size);
+  if (n_workers <= 0) return fail(NSD_ERR_INVALID, "plan: n_workers=%d", n_workers);
+  if (bt_rows <= 0 || bt_stride <= 0)
+    return fail(NSD_ERR_INVALID, "plan: block table shape [%lld, %lld]", (long long)bt_rows,
+                (long long)bt_stride);
+  const int gqa = num_q_heads / num_kv_heads;
+  if (gqa > kMaxGroupRows)
+    return fail(NSD_ERR_UNSUPPORTED, "plan: GQA group %d > %d", gqa, kMaxGroupRows);
+  if (max_group_rows < 0 || max_group_rows > kMaxGroupRows)
+    return fail(NSD_ERR_INVALID, "plan: max_group_rows=%d outside [0, %d]", max_group_rows,
+                kMaxGroupRows);
+  const int64_t max_q = std::max(1, (max_group_rows == 0 ? kMaxGroupRows : max_group_rows) / gqa);
+  const int64_t max_len = bt_stride * block_size;
+
+  // 1. verify groups: runs of rows with one seq_id and seq_len rising by one.
+  std::vector<int32_t> groups;  // {row_start, q_len, seq_id, ctx}
+  int rows_max = 0;
+  for (int64_t r = 0; r < n_rows;) {
+    const int64_t sid = seq_ids[r], sl = seq_lens[r];
+    if (sid < 0 || sid >= bt_rows)
+      return fail(NSD_ERR_INVALID, "plan: row %lld seq_id=%lld outside [0, %lld)", (long long)r,
+                  (long long)sid, (long long)bt_rows);
+    if (sl < 1 || sl > max_len)
+      return fail(NSD_ERR_INVALID, "plan: row %lld seq_len=%lld outside [1, %lld]", (long long)r,
+                  (long long)sl, (long long)max_len);
+    int64_t q = 1;
+    while (r + q < n_rows && q < max_q && seq_ids[r + q] == sid && seq_lens[r + q] == sl + q) ++q;
+    groups.insert(groups.end(), {(int32_t)r, (int32_t)q, (int32_t)sid, (int32_t)(sl - 1)});
+    rows_max = std::max<int>(rows_max, (int)(q * gqa));
+    r += q;
+  }
+  const int64_t n_groups = (int64_t)groups.size() / 4;
+  const int64_t n_segs = n_groups * num_kv_heads;
+
+  // 2. chunk counts per segment (segment = group * Hkv + kv head).
+  std::vector<int64_t> seg_start(n_segs + 1, 0);
+  for (int64_t s = 0; s < n_segs; ++s) {
+    const int32_t* g = &groups[4 * (s / num_kv_heads)];
+    const int64_t tokens = (int64_t)g[3] + g[1];
+    seg_start[s + 1] = seg_start[s] + (tokens + kChunkTokens - 1) / kChunkTokens;
+  }
+  const int64_t total = seg_start[n_segs];
+
+  // 3. equal contiguous chunk ranges per worker.
+  int64_t active = std::min<int64_t>(n_workers, (total + kMinChunksPerWorker - 1) / kMinChunksPerWorker);
+  const int64_t grid = total > 0 ? round_up8(std::max<int64_t>(active, 1)) : 0;
+  if (total == 0) active = 0;
+  std::vector<int32_t> wstart(grid + 1, 0);
+  std::vector<int32_t> pieces;  // {segment, chunk_begin, chunk_end, slot}
+  int64_t seg = 0;
+  for (int64_t w = 0; w < grid; ++w) {
+    wstart[w] = (int32_t)(pieces.size() / 4);
+    if (w >= active) continue;
+    int64_t a = total * w / active;
+    const int64_t b = total * (w + 1) / active;
+    while (a < b) {
+      while (seg_start[seg + 1] <= a) ++seg;
+      const int64_t end = std::min(b, seg_start[seg + 1]);
+      pieces.insert(pieces.end(), {(int32_t)seg, (int32_t)(a - seg_start[seg]),
+                                   (int32_t)(end - seg_start[seg]), -1});
+      a = end;
+    }
+  }
+  wstart[grid] = (int32_t)(pieces.size() / 4);
+  const int64_t n_pieces = (int64_t)pieces.size() / 4;
+
+  // 4. partial slots for segments cut into several pieces (pieces of one
+  //    segment are adjacent because workers walk the chunk stream in order).
+  std::vector<int32_t> combines;  // {segment, first_slot, n_slots, 0}
+  int64_t n_slots = 0;
+  for (int64_t i = 0; i < n_pieces;) {
+    int64_t j = i + 1;
+    while (j < n_pieces && pieces[4 * j] == pieces[4 * i]) ++j;
+    if (j - i > 1) {
+      combines.insert(combines.end(), {pieces[4 * i], (int32_t)n_slots, (int32_t)(j - i), 0});
+      for (int64_t k = i; k < j; ++k) pieces[4 * k + 3] = (int32_t)(n_slots++);
+    }
+    i = j;
+  }
+  const int64_t n_combines = (int64_t)combines.size() / 4;
+
+  const int64_t off_groups = NSD_PLAN_HEADER_WORDS;
+  const int64_t off_wstart = off_groups + 4 * n_groups;
+  const int64_t off_pieces = off_wstart + grid + 1;
+  const int64_t off_combines = off_pieces + 4 * n_pieces;
+  const int64_t words = off_combines + 4 * n_combines;
+  if (words > plan_capacity)
+    return fail(NSD_ERR_WORKSPACE, "plan: needs %lld words, capacity %lld", (long long)words,
+                (long long)plan_capacity);
+  if (words > INT32_MAX || n_slots > INT32_MAX / kMaxGroupRows)
+    return fail(NSD_ERR_INVALID, "plan: too large (%lld words)", (long long)words);
+
+  int32_t* h = plan;
+  h[kPlanMagic] = kPlanMagicValue;
+  h[kPlanVersion] = 1;
+  h[kPlanRows] = (int32_t)n_rows;
+  h[kPlanGroups] = (int32_t)n_groups;
+  h[kPlanPieces] = (int32_t)n_pieces;
+  h[kPlanWorkers] = (int32_t)grid;
+  h[kPlanCombines] = (int32_t)n_combines;
+  h[kPlanSlots] = (int32_t)n_slots;
+  h[kPlanRowsMax] = rows_max;
+  h[kPlanHq] = num_q_heads;
+  h[kPlanHkv] = num_kv_heads;
+  h[kPlanOffGroups] = (int32_t)off_groups;
+  h[kPlanOffWorkerStart] = (int32_t)off_wstart;
+  h[kPlanOffPieces] = (int32_t)off_pieces;
+  h[kPlanOffCombines] = (int32_t)off_combines;
+  h[kPlanWords] = (int32_t)words;
+  std::copy(groups.begin(), groups.end(), h + off_groups);
+  std::copy(wstart.begin(), wstart.end(), h + off_wstart);
+  std::copy(pieces.begin(), pieces.end(), h + off_pieces);
+  std::copy(combines.begin(), combines.end(), h + off_combines);
+
+  *plan_words = words;
+  const int64_t part_bytes = n_slots * rows_max * (int64_t)(kHeadDim + 1) * 4;
+  *workspace_bytes = (part_bytes + 255) / 256 * 256;
+  return NSD_OK;
+}

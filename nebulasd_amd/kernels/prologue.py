@@ -1,0 +1,59 @@
+"""Fused attention prologue: QK-RMSNorm + RoPE + KV store in one launch.
+
+Replaces the sequence of swiftLLM/swiftllm/worker/layers/transformer_layer.py:114-145
+(``rmsnorm_inplace(q)``, ``rmsnorm_inplace(k)``, ``rotary_embedding_inplace``,
+``store_kvcache``) for the decode/verify rows of a forward.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._util import StatusWord, cache_dims, ptr, require, require_cuda, stream_of
+
+
+def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, block_table: torch.Tensor, q_norm: torch.Tensor | None,
+                       k_norm: torch.Tensor | None, model_config, engine_config, infer_state,
+                       cur_layer: int, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                       validate: bool = False) -> None:
+    """Prologue of the decode/verify rows.
+
+    ``q`` [rows, Hq, d], ``k``/``v`` [rows, Hkv, d] fp16 are the decode-row
+    slices (``x[num_prefill_tokens:]``); q and k are normalised and rotated
+    in place at position ``decoding_seq_lens - 1``; K (rotated) and V are
+    stored into the cache slot of each row.  ``cos_cache``/``sin_cache`` are
+    the full [max_positions, d/2] fp16 tables (model.py:242-252).  Pass
+    ``q_norm = k_norm = None`` for models without QK-norm.
+    """
+    require_cuda(q, k, v, k_cache, v_cache, block_table, cos_cache, sin_cache, q_norm, k_norm)
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache"),
+                 (cos_cache, "cos_cache"), (sin_cache, "sin_cache")):
+        require(t, torch.float16, n)
+    require(block_table, torch.int32, "block_table")
+    if (q_norm is None) != (k_norm is None):
+        raise ValueError("pass both q_norm and k_norm, or neither")
+    if q_norm is not None:
+        require(q_norm, torch.float16, "q_norm")
+        require(k_norm, torch.float16, "k_norm")
+    n_blocks, n_layers, hkv, bs, d = cache_dims(k_cache)
+    rows = infer_state.num_decoding_seqs
+    hq = model_config.num_q_heads
+    if q.shape != (rows, hq, d) or k.shape != (rows, hkv, d) or v.shape != k.shape:
+        raise ValueError(f"q [{rows},{hq},{d}], k/v [{rows},{hkv},{d}] expected")
+    if cos_cache.dim() != 2 or cos_cache.shape[1] != d // 2 or sin_cache.shape != cos_cache.shape:
+        raise ValueError("cos/sin caches must be [max_positions, head_dim/2]")
+    if rows == 0:
+        return
+    npf = infer_state.num_prefill_seqs
+    status = StatusWord(q.device) if validate else None
+    _lib.call("nsd_qk_norm_rope_store",
+              q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(q_norm), ptr(k_norm),
+              float(model_config.rms_norm_eps), cos_cache.data_ptr(), sin_cache.data_ptr(),
+              cos_cache.shape[0], k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+              block_table.shape[0], block_table.shape[1], infer_state.seq_ids[npf:].data_ptr(),
+              infer_state.decoding_seq_lens.data_ptr(), rows, n_blocks, n_layers, int(cur_layer),
+              hq, hkv, d, bs, ptr(status.t) if status else None, stream_of(q))
+    if status is not None:
+        status.check("qk_norm_rope_store")

@@ -1,0 +1,131 @@
+"""Per-forward attention work plan (host side).
+
+The reference re-derives its launch grid on every layer call from a split
+size chosen once per forward (swiftLLM/swiftllm/worker/model.py:365-384,
+kernels/paged_attn.py:182-211).  Here the whole work decomposition -- verify
+groups, per-workgroup chunk ranges and partial slots -- is computed once per
+forward by the native planner ``nsd_attn_plan_build`` from the host copies of
+the decode rows' seq_ids / seq_lens, uploaded once, and reused by every layer.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+
+_workers_cache: dict[tuple[int, int], int] = {}
+
+
+def num_workers(max_rows: int, device_index: int | None = None) -> int:
+    """Workgroups that fill the current GPU for plans with ``max_rows`` rows per group."""
+    import torch
+
+    dev = torch.cuda.current_device() if device_index is None else device_index
+    nt = (max_rows + 15) // 16
+    key = (dev, nt)
+    if key not in _workers_cache:
+        out = ctypes.c_int(0)
+        with torch.cuda.device(dev):
+            _lib.call("nsd_attn_num_workers", 16 * nt, ctypes.byref(out))
+        _workers_cache[key] = int(out.value)
+    return _workers_cache[key]
+
+
+def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
+               block_size: int, bt_rows: int, bt_stride: int, n_workers: int,
+               max_group_rows: int = 0) -> tuple[np.ndarray, int]:
+    """Run the native planner on host lists; returns (plan words int32, workspace bytes)."""
+    sid = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int32))
+    sl = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.int32))
+    if sid.shape != sl.shape or sid.ndim != 1:
+        raise ValueError("seq_ids and seq_lens must be 1-D of equal length")
+    lib = _lib.load()
+    cap = lib.nsd_attn_plan_bound(len(sid), num_kv_heads, n_workers)
+    if cap < 0:
+        raise ValueError(f"bad plan bound arguments (rows={len(sid)}, hkv={num_kv_heads}, "
+                         f"workers={n_workers})")
+    buf = np.zeros(cap, dtype=np.int32)
+    words = ctypes.c_int64(0)
+    ws = ctypes.c_int64(0)
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    _lib.check(lib.nsd_attn_plan_build(
+        sid.ctypes.data_as(i32p), sl.ctypes.data_as(i32p), len(sid), num_q_heads, num_kv_heads,
+        head_dim, block_size, bt_rows, bt_stride, n_workers, max_group_rows,
+        buf.ctypes.data_as(i32p), cap, ctypes.byref(words), ctypes.byref(ws)),
+        "nsd_attn_plan_build")
+    return buf[: words.value].copy(), int(ws.value)
+
+
+def decode_plan(words: np.ndarray) -> dict:
+    """Split plan words into named numpy views (for inspection and tests)."""
+    h = words[:_lib.PLAN_HEADER_WORDS]
+    n_groups, n_pieces = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_PIECES])
+    n_workers, n_comb = int(h[_lib.PLAN_WORKERS]), int(h[_lib.PLAN_COMBINES])
+    og, ow = int(h[_lib.PLAN_OFF_GROUPS]), int(h[_lib.PLAN_OFF_WSTART])
+    op, oc = int(h[_lib.PLAN_OFF_PIECES]), int(h[_lib.PLAN_OFF_COMBINES])
+    return {
+        "rows": int(h[_lib.PLAN_ROWS]),
+        "workers": n_workers,
+        "slots": int(h[_lib.PLAN_SLOTS]),
+        "rows_max": int(h[_lib.PLAN_ROWS_MAX]),
+        "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
+        "worker_start": words[ow:ow + n_workers + 1],
+        "pieces": words[op:op + 4 * n_pieces].reshape(n_pieces, 4),
+        "combines": words[oc:oc + 4 * n_comb].reshape(n_comb, 4),
+    }
+
+
+@dataclass
+class AttnPlan:
+    """A plan resident on the host and on one GPU, plus its partial workspace."""
+
+    host: np.ndarray          # int32 plan words
+    dev: "object"             # torch.int32 tensor on the GPU (same words)
+    workspace: "object"       # torch.uint8 tensor (>= workspace_bytes), or None
+    workspace_bytes: int
+    num_q_heads: int
+    num_kv_heads: int
+
+    @property
+    def rows_max(self) -> int:
+        return int(self.host[_lib.PLAN_ROWS_MAX])
+
+    @property
+    def n_rows(self) -> int:
+        return int(self.host[_lib.PLAN_ROWS])
+
+    def host_ptr(self):
+        return self.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    block_size: int, bt_rows: int, bt_stride: int, device,
+                    n_workers: int | None = None, max_group_rows: int = 0) -> AttnPlan:
+    """Plan + upload for the decode rows of one forward.
+
+    ``seq_ids`` / ``seq_lens``: host sequences (the decode rows' block-table
+    rows and lengths, model.py:329-341).  ``max_group_rows = 1`` disables
+    verify grouping (pure row-wise decode, as the reference launches it).
+    """
+    import torch
+
+    device = torch.device(device)
+    gqa = num_q_heads // num_kv_heads
+    if n_workers is None:
+        # size the grid for the row-tile count the grouping will produce
+        guess = min(64, gqa * max(1, (max_group_rows or 64) // gqa))
+        n_workers = num_workers(guess, device.index)
+    words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim, block_size,
+                           bt_rows, bt_stride, n_workers, max_group_rows)
+    rows_max = int(words[_lib.PLAN_ROWS_MAX])
+    if rows_max > 0 and n_workers != num_workers(rows_max, device.index):
+        words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim,
+                               block_size, bt_rows, bt_stride,
+                               num_workers(rows_max, device.index), max_group_rows)
+    dev = torch.from_numpy(words).to(device, non_blocking=False)
+    workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=device)
+    return AttnPlan(words, dev, workspace, ws, num_q_heads, num_kv_heads)

@@ -1,0 +1,15 @@
+"""CPU oracle for the verify/decode paged-attention path.
+
+TEST INFRASTRUCTURE ONLY.  This package restates, in numpy, the algorithm of
+swiftLLM's Triton kernels for the path (paged attention, KV-cache store,
+QK-RMSNorm, RoPE) and of the host code that defines the verify rows.  It is
+imported only by ``tests/``, by ``__graft_entry__.smoke()`` (as the checker)
+and by ``bench.py``'s ``cpu_baseline`` leg (as the timed CPU baseline).  The
+product path (``nebulasd_amd``) never imports it and has no CPU fallback.
+
+Every function cites the reference file:line it follows.  How each function
+is pinned (closed forms, invariants, library routines, the reference's own
+literal test cases) is listed in ``oracle/attention.py``'s header.
+"""
+
+from .attention import *  # noqa: F401,F403

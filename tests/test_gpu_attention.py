@@ -1,0 +1,125 @@
+"""GPU parity of the paged verify/decode attention against the numpy oracle.
+
+Every case prints its name first (pytest -v) so a failing GPU step is named.
+Tolerances (written in tests/helpers.py): o within 2e-3 abs + 1e-2 rel,
+natural-log LSE within 1e-4 abs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import ATOL_LSE, ATOL_O, RTOL_O, assert_close, compact_cache
+from nebulasd_amd.config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
+from nebulasd_amd.infer_state import build_infer_state, rope_cache
+from nebulasd_amd.kernels import paged_attention
+from nebulasd_amd.workload import make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def run_attention(w, layer, max_group_rows=0, validate=True):
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)
+    st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, w.q.device, max_group_rows)
+    o = torch.empty_like(w.q)
+    lse = torch.empty(w.q.shape[:2], dtype=torch.float32, device=w.q.device)
+    paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o, lse,
+                    validate=validate)
+    torch.cuda.synchronize()
+    return o, lse, st
+
+
+def oracle_attention(w, layer):
+    kc, vc, bt = compact_cache(w.k_cache, w.v_cache, w.block_table, w.seq_ids, w.seq_lens, layer)
+    return oracle.paged_attention(w.q.cpu().numpy(), kc, vc, bt, w.seq_ids, w.seq_lens, 0)
+
+
+def check_against_oracle(w, layer, o, lse, what):
+    wo, wl = oracle_attention(w, layer)
+    e_o = assert_close(o.float().cpu().numpy(), wo, ATOL_O, RTOL_O, f"{what} o")
+    e_l = assert_close(lse.cpu().numpy(), wl, ATOL_LSE, 0.0, f"{what} lse")
+    print(f"{what}: max|do|={e_o:.2e} max|dlse|={e_l:.2e}", flush=True)
+
+
+CASES = [("cpu_plumbing", 0), ("cpu_plumbing", 1), ("cpu_plumbing", 2), ("draft_decode", 0),
+         ("target_verify", 0), ("target_verify", 1), ("ragged_verify", 0)]
+
+
+@pytest.mark.parametrize("name,seed", CASES, ids=[f"{n}-s{s}" for n, s in CASES])
+def test_attention_matches_oracle(gpu, name, seed):
+    w = make_workload(name, seed, device=gpu)
+    layer = w.spec.num_layers // 2
+    o, lse, st = run_attention(w, layer)
+    check_against_oracle(w, layer, o, lse, f"{name} seed {seed}")
+    if name == "target_verify":
+        # the reference's row-wise launch (no verify grouping) gives the same result
+        o1, l1, _ = run_attention(w, layer, max_group_rows=1)
+        check_against_oracle(w, layer, o1, l1, f"{name} seed {seed} row-wise")
+    del w
+    torch.cuda.empty_cache()
+
+
+EDGE_CTXS = [0, 1, 14, 15, 16, 17, 30, 31, 32, 33, 47, 63, 64, 65, 100, 127, 128, 257]
+
+
+@pytest.mark.parametrize("model,q_len", [(QWEN3_8B, 1), (QWEN3_8B, 5), (QWEN3_8B, 9),
+                                         (QWEN3_8B, 16), (QWEN3_8B, 17), (QWEN3_0_6B, 1),
+                                         (QWEN3_0_6B, 5), (QWEN3_0_6B, 32)],
+                         ids=["8b-q1", "8b-q5", "8b-q9", "8b-q16", "8b-q17", "06b-q1", "06b-q5",
+                              "06b-q32"])
+def test_attention_chunk_boundaries(gpu, model, q_len):
+    """Contexts on both sides of the 16-token block and 32-token chunk edges."""
+    w = make_workload("target_verify", 3, device=gpu, pool_blocks=600, num_layers=3,
+                      ctxs=EDGE_CTXS, q_len=q_len, model=model)
+    o, lse, _ = run_attention(w, 2)
+    check_against_oracle(w, 2, o, lse, f"edges q_len={q_len}")
+
+
+def test_attention_every_layer_and_deterministic(gpu):
+    w = make_workload("target_verify", 4, device=gpu, pool_blocks=2048, num_layers=4,
+                      ctxs=[300, 1000, 77, 2500])
+    for layer in range(4):
+        o, lse, _ = run_attention(w, layer)
+        check_against_oracle(w, layer, o, lse, f"layer {layer}")
+    o2, lse2, _ = run_attention(w, 3)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+
+
+def test_attention_closed_form_single_token(gpu):
+    """seq_len = 1: the output is V of token 0 and the LSE its score."""
+    w = make_workload("target_verify", 5, device=gpu, pool_blocks=64, num_layers=2,
+                      ctxs=[0, 0, 0], q_len=1)
+    o, lse, _ = run_attention(w, 1)
+    blk = w.block_table[:, 0].long()
+    v0 = w.v_cache[blk, 1, :, 0].float()  # [3, Hkv, d]
+    k0 = w.k_cache[blk, 1, :, 0].float()
+    g = w.spec.num_q_heads // w.spec.num_kv_heads
+    want_o = v0.repeat_interleave(g, dim=1)
+    want_l = (w.q.float() * k0.repeat_interleave(g, dim=1)).sum(-1) * 128 ** -0.5
+    assert_close(o.float().cpu().numpy(), want_o.cpu().numpy(), 1e-3, 0, "seq_len=1 o")
+    assert_close(lse.cpu().numpy(), want_l.cpu().numpy(), ATOL_LSE, 0, "seq_len=1 lse")
+
+
+def test_attention_bad_block_is_flagged(gpu):
+    """An out-of-range block id is skipped by the kernel and reported, not faulted on."""
+    w = make_workload("target_verify", 6, device=gpu, pool_blocks=256, num_layers=2,
+                      ctxs=[40, 90], q_len=5)
+    w.block_table[1, 2] = w.k_cache.shape[0] + 5
+    with pytest.raises(RuntimeError, match="block id outside the pool"):
+        run_attention(w, 0, validate=True)
+
+
+def test_attention_no_rows(gpu):
+    mc = ModelConfig(QWEN3_8B)
+    ec = EngineConfig()
+    cos, sin = rope_cache(128, 1e6, 8, gpu)
+    st = build_infer_state([], [], [], mc, cos, sin, gpu)
+    kc = torch.zeros((4, 1, 8, 16, 128), dtype=torch.float16, device=gpu)
+    q = torch.empty((0, 32, 128), dtype=torch.float16, device=gpu)
+    paged_attention(q, kc, kc, torch.zeros((1, 4), dtype=torch.int32, device=gpu), mc, ec, st, 0,
+                    torch.empty_like(q))

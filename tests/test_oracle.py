@@ -1,0 +1,308 @@
+"""Pins for the numpy oracle (CPU only).
+
+Each oracle function is checked against something it does not restate:
+the reference's own literal test cases, a library routine (torch SDPA,
+torch rms_norm), closed forms, or numpy's own indexing.  The mutant tests at
+the end plant plausible mistakes in the oracle's inputs/outputs and show
+that these pins reject them.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "speculative_cases.json").read_text())
+
+
+# ---------------------------------------------------------------- row expansion
+
+def test_linear_rows_golden():
+    for case in GOLDEN["linear_rows"]:
+        toks, lens = oracle.build_linear_verification_rows(
+            case["prompt_len"], case["output_token_ids"], case["draft_token_ids"])
+        assert toks == case["expect_tokens"]
+        assert lens == case["expect_seq_lens"]
+
+
+def test_expand_verify_rows_matches_linear_rows():
+    # backend.py:101-110 with logical = prompt_len + len(output) - 1 reproduces speculative.py:75-89
+    case = GOLDEN["linear_rows"][0]
+    logical = case["prompt_len"] + len(case["output_token_ids"]) - 1
+    ids, sids, lens = oracle.expand_verify_rows([(3, logical, case["output_token_ids"][-1],
+                                                  case["draft_token_ids"])])
+    assert ids == case["expect_tokens"] and lens == case["expect_seq_lens"] and sids == [3] * 4
+
+
+def test_greedy_acceptance_golden():
+    for case in GOLDEN["greedy_acceptance"]:
+        got = oracle.compute_greedy_acceptance(case["draft"], case["posterior"], case["remaining"],
+                                               case["stops"])
+        assert got == (case["expect"], case["count"]), case["_ref"]
+    neg = GOLDEN["negative_remaining"]
+    with pytest.raises(ValueError, match=neg["error"]):
+        oracle.compute_greedy_acceptance(neg["draft"], neg["posterior"], neg["remaining"])
+
+
+def test_aggregate_golden():
+    c = GOLDEN["aggregate_max_lens"]
+    got = oracle.aggregate_max_lens_by_seq_id(c["seq_ids"], c["seq_lens"])
+    assert got == {int(k): v for k, v in c["expect"].items()}
+
+
+# ---------------------------------------------------------------- KV placement
+
+def _small_cache(rng, blocks=12, layers=3, hkv=2, bs=16, d=8):
+    return rng.standard_normal((blocks, layers, hkv, bs, d)).astype(np.float16)
+
+
+def test_slot_offset_matches_numpy_indexing():
+    rng = np.random.default_rng(0)
+    kc = _small_cache(rng)
+    bt = rng.permutation(12).reshape(3, 4)
+    flat = kc.reshape(-1)
+    for sid in range(3):
+        for pos in range(64):
+            for layer in range(3):
+                for h in range(2):
+                    off = oracle.kv_slot_offset(bt, sid, pos, layer, h, 3, 2, 16, 8)
+                    np.testing.assert_array_equal(flat[off:off + 8],
+                                                  kc[bt[sid, pos // 16], layer, h, pos % 16])
+
+
+def test_store_kvcache_canary():
+    rng = np.random.default_rng(1)
+    kc = np.full((12, 3, 2, 16, 8), 7.0, np.float16)
+    vc = np.full_like(kc, -3.0)
+    bt = rng.permutation(12).reshape(3, 4)
+    seq_ids, seq_lens = [0, 0, 2, 1], [5, 6, 33, 64]
+    k = rng.standard_normal((4, 2, 8)).astype(np.float16)
+    v = rng.standard_normal((4, 2, 8)).astype(np.float16)
+    kc2, vc2 = kc.copy(), vc.copy()
+    oracle.store_kvcache(k, v, kc2, vc2, bt, seq_ids, seq_lens, layer=1)
+    want_k, want_v = kc.reshape(-1).copy(), vc.reshape(-1).copy()
+    for r in range(4):
+        for h in range(2):
+            off = oracle.kv_slot_offset(bt, seq_ids[r], seq_lens[r] - 1, 1, h, 3, 2, 16, 8)
+            want_k[off:off + 8] = k[r, h]
+            want_v[off:off + 8] = v[r, h]
+    assert kc2.reshape(-1).tobytes() == want_k.tobytes()
+    assert vc2.reshape(-1).tobytes() == want_v.tobytes()
+
+
+def test_store_prefill_equals_decode_rows():
+    # a prefill of n tokens writes the same slots as n decode rows with seq_len 1..n
+    rng = np.random.default_rng(2)
+    bt = rng.permutation(12).reshape(3, 4)
+    k = rng.standard_normal((40, 2, 8)).astype(np.float16)
+    v = rng.standard_normal((40, 2, 8)).astype(np.float16)
+    a = [np.zeros((12, 3, 2, 16, 8), np.float16) for _ in range(2)]
+    b = [np.zeros((12, 3, 2, 16, 8), np.float16) for _ in range(2)]
+    oracle.store_kvcache_prefill(k, v, a[0], a[1], bt, [1, 2], [17, 23], layer=2)
+    oracle.store_kvcache(k, v, b[0], b[1], bt, [1] * 17 + [2] * 23,
+                         list(range(1, 18)) + list(range(1, 24)), layer=2)
+    assert a[0].tobytes() == b[0].tobytes() and a[1].tobytes() == b[1].tobytes()
+
+
+# ---------------------------------------------------------------- QK-norm / RoPE
+
+def test_rmsnorm_matches_torch():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 128)) * 3).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 128).astype(np.float16)
+    got = oracle.rmsnorm(x, w, 1e-6).astype(np.float32)
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (128,),
+                                        torch.from_numpy(w).double(), eps=1e-6).numpy()
+    # one fp16 rounding of the result: within 1 ulp
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -10 + 1e-7)
+
+
+def test_rmsnorm_constant_row_closed_form():
+    w = np.linspace(0.5, 1.5, 128).astype(np.float16)
+    for c in (-2.5, 0.25, 7.0):
+        x = np.full((1, 128), c, np.float16)
+        got = oracle.rmsnorm(x, w, 0.0)
+        np.testing.assert_array_equal(got[0], (np.sign(c) * w.astype(np.float32)).astype(np.float16))
+
+
+def test_rope_table_closed_forms():
+    cos, sin = oracle.rope_cache(128, 1e6, 4096)
+    pos = np.arange(4096)
+    # frequency 0 has inv_freq = 1: cos(pos), sin(pos)
+    np.testing.assert_allclose(cos[:, 0].astype(np.float64), np.cos(pos), atol=1e-3)
+    np.testing.assert_allclose(sin[:, 0].astype(np.float64), np.sin(pos), atol=1e-3)
+    c, s = cos.astype(np.float64), sin.astype(np.float64)
+    np.testing.assert_allclose(c * c + s * s, 1.0, atol=2e-3)
+    np.testing.assert_array_equal(cos[0], 1.0)
+    np.testing.assert_array_equal(sin[0], 0.0)
+    # last frequency: theta^(-126/128)
+    f = 1e6 ** (-126 / 128)
+    np.testing.assert_allclose(cos[4000, 63], math.cos(4000 * f), atol=1e-3)
+
+
+def test_rope_identity_norm_and_complex_form():
+    rng = np.random.default_rng(4)
+    cos, sin = oracle.rope_cache(128, 1e6, 2048)
+    x = rng.standard_normal((16, 4, 128)).astype(np.float16)
+    pos = rng.integers(0, 2048, 16)
+    pos[0] = 0
+    y = oracle.rope(x, cos[pos], sin[pos])
+    np.testing.assert_array_equal(y[0], x[0])  # position 0 is the identity
+    # complex form: (x0 + i x1) * (cos + i sin)
+    z = (x[..., :64].astype(np.float64) + 1j * x[..., 64:].astype(np.float64)) * \
+        (cos[pos].astype(np.float64) + 1j * sin[pos].astype(np.float64))[:, None, :]
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    np.testing.assert_allclose(y.astype(np.float64), want, atol=4e-3, rtol=2e-3)
+    n_in = np.hypot(x[..., :64].astype(np.float64), x[..., 64:].astype(np.float64))
+    n_out = np.hypot(y[..., :64].astype(np.float64), y[..., 64:].astype(np.float64))
+    np.testing.assert_allclose(n_out, n_in, atol=4e-3, rtol=3e-3)
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_case(seed=0, hq=8, hkv=2, d=32, bs=16, layers=2, blocks=40, lens=(1, 17, 33, 70, 70, 71)):
+    rng = np.random.default_rng(seed)
+    kc = rng.standard_normal((blocks, layers, hkv, bs, d)).astype(np.float16)
+    vc = rng.standard_normal((blocks, layers, hkv, bs, d)).astype(np.float16)
+    bt = rng.permutation(blocks)[:4 * 8].reshape(4, 8)
+    seq_ids = [0, 1, 2, 3, 3, 3][: len(lens)]
+    q = rng.standard_normal((len(lens), hq, d)).astype(np.float16)
+    return q, kc, vc, bt, seq_ids, list(lens)
+
+
+def sdpa_reference(q, kc, vc, bt, seq_ids, seq_lens, layer, scale=None):
+    """torch SDPA on K/V gathered with torch indexing and GQA via repeat_interleave
+    (the reference's commented loop, paged_attn.py:224-259)."""
+    rows, hq, d = q.shape
+    hkv, bs = kc.shape[2], kc.shape[3]
+    scale = d ** -0.5 if scale is None else scale
+    K, V, Q = torch.from_numpy(kc).double(), torch.from_numpy(vc).double(), torch.from_numpy(q).double()
+    os, ls = [], []
+    for r in range(rows):
+        n = seq_lens[r]
+        ids = torch.from_numpy(np.asarray(bt[seq_ids[r], : (n + bs - 1) // bs], dtype=np.int64))
+        k = torch.cat(list(K[ids, layer]), dim=1)[:, :n]  # [Hkv, n, d]
+        v = torch.cat(list(V[ids, layer]), dim=1)[:, :n]
+        k = k.repeat_interleave(hq // hkv, dim=0)
+        v = v.repeat_interleave(hq // hkv, dim=0)
+        qq = Q[r][:, None, :]
+        o = torch.nn.functional.scaled_dot_product_attention(qq, k, v, scale=scale)[:, 0]
+        s = (qq @ k.transpose(1, 2))[:, 0] * scale
+        os.append(o.numpy())
+        ls.append(torch.logsumexp(s, dim=-1).numpy())
+    return np.stack(os), np.stack(ls)
+
+
+def test_attention_matches_sdpa():
+    q, kc, vc, bt, sids, lens = _attn_case()
+    o, lse = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=1)
+    wo, wl = sdpa_reference(q, kc, vc, bt, sids, lens, layer=1)
+    np.testing.assert_allclose(o, wo, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(lse, wl, atol=1e-12, rtol=1e-12)
+
+
+def test_attention_bruteforce_tiny():
+    q, kc, vc, bt, sids, lens = _attn_case(seed=5, hq=4, hkv=2, d=4, lens=(3, 18))
+    o, lse = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=0)
+    for r, (sid, n) in enumerate(zip(sids, lens)):
+        for qh in range(4):
+            kv = qh // 2
+            sc = []
+            for t in range(n):
+                blk = bt[sid, t // 16]
+                sc.append(sum(float(q[r, qh, i]) * float(kc[blk, 0, kv, t % 16, i]) for i in range(4)) * 0.5)
+            mx = max(sc)
+            e = [math.exp(x - mx) for x in sc]
+            tot = sum(e)
+            for i in range(4):
+                want = sum(e[t] * float(vc[bt[sid, t // 16], 0, kv, t % 16, i]) for t in range(n)) / tot
+                assert abs(o[r, qh, i] - want) < 1e-12
+            assert abs(lse[r, qh] - (math.log(tot) + mx)) < 1e-12
+
+
+def test_attention_closed_forms():
+    q, kc, vc, bt, sids, lens = _attn_case(seed=6)
+    # seq_len = 1 -> o = v of token 0, lse = its score
+    o, lse = oracle.paged_attention(q[:1], kc, vc, bt, [0], [1], layer=0)
+    blk = bt[0, 0]
+    for qh in range(8):
+        np.testing.assert_allclose(o[0, qh], vc[blk, 0, qh // 4, 0].astype(np.float64), atol=1e-12)
+        want = float(q[0, qh].astype(np.float64) @ kc[blk, 0, qh // 4, 0].astype(np.float64)) * 32 ** -0.5
+        assert abs(lse[0, qh] - want) < 1e-12
+    # identical keys -> mean of V, lse = s + ln(n)
+    kc2 = kc.copy()
+    kc2[:, :, :, :, :] = kc[0, 0, :, 0][None, None, :, None, :]
+    n = 45
+    o, lse = oracle.paged_attention(q[:1], kc2, vc, bt, [1], [n], layer=1)
+    _, vv = oracle.gather_kv(kc2, vc, bt, 1, n, 1)
+    for qh in range(8):
+        np.testing.assert_allclose(o[0, qh], vv[qh // 4].mean(0), atol=1e-12)
+    # one dominant logit -> that token's V
+    kc3 = kc.copy()
+    t = 29
+    kc3[bt[2, t // 16], 0, :, t % 16] = (q[2].reshape(2, 4, 32).astype(np.float32).sum(1) * 60).astype(np.float16)
+    o, _ = oracle.paged_attention(q[2:3], kc3, vc, bt, [2], [33], layer=0)
+    for qh in range(8):
+        np.testing.assert_allclose(o[0, qh], vc[bt[2, t // 16], 0, qh // 4, t % 16].astype(np.float64), atol=1e-6)
+
+
+def test_grouped_equals_rowwise():
+    q, kc, vc, bt, sids, lens = _attn_case(seed=7)
+    o, lse = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=1)
+    for r in range(len(lens)):
+        o1, l1 = oracle.paged_attention(q[r:r + 1], kc, vc, bt, sids[r:r + 1], lens[r:r + 1], layer=1)
+        np.testing.assert_allclose(o[r], o1[0], atol=1e-13)
+        np.testing.assert_allclose(lse[r], l1[0], atol=1e-13)
+
+
+@pytest.mark.parametrize("sbs", [16, 32, 64, 2048])
+def test_two_phase_split_invariance(sbs):
+    q, kc, vc, bt, sids, lens = _attn_case(seed=8)
+    o, lse = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=0)
+    o2, l2 = oracle.paged_attention_two_phase(q, kc, vc, bt, sids, lens, 0, sbs)
+    np.testing.assert_allclose(o2, o, atol=1e-12)
+    np.testing.assert_allclose(l2, lse, atol=1e-12)
+
+
+def test_reference_split_heuristic():
+    # model.py:380-384: halves from 2048 while Hkv*sum/sbs < 1024 (bounded by 64 and max/sbs <= 128)
+    assert oracle.reference_seq_block_size(8, [2048] * 16) == 256   # 8*32768/256 = 1024
+    assert oracle.reference_seq_block_size(8, [100] * 4) == 64      # floor of 64
+    assert oracle.reference_seq_block_size(1, [32768]) == 256       # max_len/sbs <= 128 bound
+
+
+# ---------------------------------------------------------------- planted mistakes
+
+def _pin_rejects(q, kc, vc, bt, sids, lens, o_bad, lse_bad):
+    wo, wl = sdpa_reference(q, kc, vc, bt, sids, lens, layer=1)
+    return not (np.allclose(o_bad, wo, atol=2e-3, rtol=1e-2) and np.allclose(lse_bad, wl, atol=1e-4))
+
+
+def test_pins_reject_planted_mistakes():
+    q, kc, vc, bt, sids, lens = _attn_case(seed=9)
+    # (1) GQA mapping qh % Hkv instead of qh // G: permute q heads accordingly
+    hq, hkv = 8, 2
+    perm = [(qh % hkv) * (hq // hkv) + qh // hkv for qh in range(hq)]
+    o, l = oracle.paged_attention(q[:, perm], kc, vc, bt, sids, lens, layer=1)
+    inv = np.argsort(perm)
+    assert _pin_rejects(q, kc, vc, bt, sids, lens, o[:, inv], l[:, inv])
+    # (2) off-by-one length (the new token not attended)
+    lens_m = [max(1, n - 1) for n in lens]
+    o, l = oracle.paged_attention(q, kc, vc, bt, sids, lens_m, layer=1)
+    assert _pin_rejects(q, kc, vc, bt, sids, lens, o, l)
+    # (3) wrong layer
+    o, l = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=0)
+    assert _pin_rejects(q, kc, vc, bt, sids, lens, o, l)
+    # (4) missing softmax scale
+    o, l = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=1, softmax_scale=1.0)
+    assert _pin_rejects(q, kc, vc, bt, sids, lens, o, l)
+    # (5) LSE in log2 instead of ln
+    o, l = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=1)
+    assert _pin_rejects(q, kc, vc, bt, sids, lens, o, l / oracle.LN2)

@@ -1,0 +1,219 @@
+"""Host-side tests of the C-ABI library (no GPU calls): symbol exports,
+argument validation, and the attention planner's invariants."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nsd_attn.h"
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "speculative_cases.json").read_text())
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nebulasd_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from nebulasd_amd.build import build
+
+        build()
+    return _lib.load()
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(nsd_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol(lib):
+    from nebulasd_amd import _lib
+
+    names = header_functions()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in nsd_attn.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.nsd_version() >= 100
+
+
+def test_error_paths_without_gpu(lib):
+    from nebulasd_amd import _lib
+
+    # unsupported head_dim is rejected before any HIP call
+    rc = lib.nsd_store_kvcache(None, None, None, None, None, 1, 1, None, None, 1, 1, 1, 0, 8, 64,
+                               16, None, None)
+    assert rc == 2 and "head_dim=64" in _lib.last_error()
+    rc = lib.nsd_store_kvcache(None, None, None, None, None, 1, 1, None, None, 1, 1, 2, 5, 8, 128,
+                               16, None, None)
+    assert rc == 1 and "layer=5" in _lib.last_error()
+    rc = lib.nsd_rmsnorm_inplace(None, None, 4, 128, 1e-6, None)
+    assert rc == 1 and "null" in _lib.last_error()
+    # zero rows: nothing to launch
+    assert lib.nsd_rmsnorm_inplace(None, None, 0, 128, 1e-6, None) == 0
+    plan = np.zeros(16, np.int32)
+    rc = lib.nsd_paged_attention(None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
+                                 plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, None, 0,
+                                 0.1, None, None)
+    assert rc == 1 and "null plan" in _lib.last_error()
+    rc = lib.nsd_paged_attention(None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
+                                 plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                 plan.ctypes.data, None, 0, 0.1, None, None)
+    assert rc == 1 and "not a plan" in _lib.last_error()
+
+
+def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
+    from nebulasd_amd.plan import decode_plan, plan_words
+
+    words, ws = plan_words(seq_ids, seq_lens, hq, hkv, 128, 16, bt_rows or (max(seq_ids) + 1),
+                           stride, workers, max_group_rows)
+    return decode_plan(words), ws
+
+
+def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
+    groups, pieces, ws = p["groups"], p["pieces"], p["worker_start"]
+    # groups tile the rows in order with seq_len rising by one inside a group
+    r = 0
+    for row_start, q_len, sid, ctx in groups:
+        assert row_start == r and q_len >= 1 and q_len * gqa <= 64
+        for i in range(q_len):
+            assert seq_ids[r + i] == sid and seq_lens[r + i] == ctx + 1 + i
+        r += q_len
+    assert r == len(seq_lens)
+    # every (segment, chunk) covered exactly once, workers walk the stream in order
+    chunks = [(-(-(int(g[3]) + int(g[1])) // 32)) for g in groups for _ in range(hkv)]
+    covered = [np.zeros(n, int) for n in chunks]
+    last = (-1, -1)
+    for w in range(p["workers"]):
+        for pc in range(ws[w], ws[w + 1]):
+            seg, cb, ce, slot = (int(x) for x in pieces[pc])
+            assert 0 <= cb < ce <= chunks[seg]
+            assert (seg, cb) > last
+            last = (seg, ce - 1)
+            covered[seg][cb:ce] += 1
+    assert all((c == 1).all() for c in covered)
+    # slots exactly for segments cut into several pieces
+    per_seg = {}
+    for seg, cb, ce, slot in pieces:
+        per_seg.setdefault(int(seg), []).append(int(slot))
+    combined = {int(c[0]): (int(c[1]), int(c[2])) for c in p["combines"]}
+    for seg, slots in per_seg.items():
+        if len(slots) == 1:
+            assert slots == [-1] and seg not in combined
+        else:
+            first, n = combined[seg]
+            assert slots == list(range(first, first + n))
+    # near-equal work per active worker
+    work = [sum(int(pieces[pc][2] - pieces[pc][1]) for pc in range(ws[w], ws[w + 1]))
+            for w in range(p["workers"])]
+    active = [x for x in work if x > 0]
+    assert max(active) - min(active) <= 1
+    assert p["workers"] % 8 == 0
+
+
+def test_plan_groups_reference_literal_rows(lib):
+    case = GOLDEN["linear_rows"][0]
+    p, _ = _plan([3, 3, 3, 3], case["expect_seq_lens"])
+    assert p["groups"].tolist() == [[0, 4, 3, 102]]
+    check_plan_invariants(p, [3] * 4, case["expect_seq_lens"], 8, 4)
+
+
+def test_plan_rowwise_mode(lib):
+    lens = [103, 104, 105, 106]
+    p, _ = _plan([3] * 4, lens, max_group_rows=1)
+    assert p["groups"].tolist() == [[i, 1, 3, lens[i] - 1] for i in range(4)]
+    check_plan_invariants(p, [3] * 4, lens, 8, 4)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_plan_invariants_random(lib, seed):
+    rng = np.random.default_rng(seed)
+    seq_ids, seq_lens = [], []
+    for sid in range(rng.integers(1, 40)):
+        ctx = int(rng.integers(0, 5000))
+        q = int(rng.integers(1, 20))
+        seq_ids += [sid] * q
+        seq_lens += list(range(ctx + 1, ctx + q + 1))
+    # a broken run (not rising by one) must split into groups
+    seq_ids += [99, 99]
+    seq_lens += [50, 50]
+    workers = int(rng.choice([8, 64, 256, 1000]))
+    for hq, hkv in ((32, 8), (16, 8), (8, 8)):
+        p, ws = _plan(seq_ids, seq_lens, hq, hkv, workers, bt_rows=100)
+        check_plan_invariants(p, seq_ids, seq_lens, hkv, hq // hkv)
+        assert ws >= p["slots"] * p["rows_max"] * 129 * 4
+
+
+def test_plan_splits_long_groups(lib):
+    # q_len 20 with GQA 4 -> 80 rows > 64: split into 16 + 4
+    lens = list(range(501, 521))
+    p, _ = _plan([0] * 20, lens)
+    assert p["groups"].tolist() == [[0, 16, 0, 500], [16, 4, 0, 516]]
+    assert p["rows_max"] == 64
+
+
+@pytest.mark.parametrize("bad", [
+    dict(seq_lens=[0]), dict(seq_lens=[4097]), dict(seq_ids=[5]), dict(seq_ids=[-1]),
+])
+def test_plan_rejects_bad_rows(lib, bad):
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import plan_words
+
+    args = dict(seq_ids=[0], seq_lens=[10])
+    args.update(bad)
+    with pytest.raises(_lib.NativeLibraryError):
+        plan_words(args["seq_ids"], args["seq_lens"], 32, 8, 128, 16, 2, 256, 64)
+
+
+def test_plan_rejects_unsupported_shapes(lib):
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import plan_words
+
+    with pytest.raises(_lib.NativeLibraryError, match="head_dim"):
+        plan_words([0], [10], 32, 8, 64, 16, 1, 256, 64)
+    with pytest.raises(_lib.NativeLibraryError, match="block_size"):
+        plan_words([0], [10], 32, 8, 128, 32, 1, 256, 64)
+    with pytest.raises(_lib.NativeLibraryError, match="multiple"):
+        plan_words([0], [10], 30, 8, 128, 16, 1, 256, 64)
+
+
+def test_plan_empty(lib):
+    from nebulasd_amd.plan import decode_plan, plan_words
+
+    words, ws = plan_words([], [], 32, 8, 128, 16, 1, 16, 64)
+    p = decode_plan(words)
+    assert p["workers"] == 0 and len(p["pieces"]) == 0 and ws == 0
+
+
+def test_package_speculative_matches_golden():
+    from nebulasd_amd import speculative as sp
+
+    for case in GOLDEN["linear_rows"]:
+        assert sp.build_linear_verification_rows(case["prompt_len"], case["output_token_ids"],
+                                                 case["draft_token_ids"]) == \
+            (case["expect_tokens"], case["expect_seq_lens"])
+    for case in GOLDEN["greedy_acceptance"]:
+        assert sp.compute_greedy_acceptance(case["draft"], case["posterior"], case["remaining"],
+                                            case["stops"]) == (case["expect"], case["count"])
+    c = GOLDEN["aggregate_max_lens"]
+    assert sp.aggregate_max_lens_by_seq_id(c["seq_ids"], c["seq_lens"]) == \
+        {int(k): v for k, v in c["expect"].items()}
+    with pytest.raises(ValueError, match="non-negative"):
+        sp.compute_greedy_acceptance([1], [1, 2], -1)
+
+
+def test_qwen3_shape_constants():
+    from nebulasd_amd.config import QWEN3_8B, ModelConfig
+
+    g = GOLDEN["qwen3_8b_shape"]
+    cfg = ModelConfig(QWEN3_8B)
+    assert (cfg.num_q_heads, cfg.num_kv_heads, cfg.hidden_size, cfg.head_dim, cfg.vocab_size) == \
+        (g["num_q_heads"], g["num_kv_heads"], g["hidden_size"], g["head_dim"], g["vocab_size"])
+    assert cfg.rope_theta == g["rope_theta"] and cfg.rms_norm_eps == g["rms_norm_eps"]
+    assert cfg.has_qk_norm
