@@ -107,6 +107,27 @@ def measure(name: str, seed: int, steps: int, warmup: int):
     return res, w
 
 
+def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Achievable HBM rate of a plain device copy (read + write bytes / time), GB/s."""
+    import torch
+
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * nbytes / sec / 1e9
+
+
 def cpu_baseline(w, budget_s: float):
     """Time the numpy oracle (fp32) on the same inputs; bounded to ~budget_s seconds."""
     import numpy as np
@@ -165,6 +186,7 @@ def main():
         from nebulasd_amd.build import build
 
         build()
+    copy_gbps = copy_probe()
     res, w = measure(args.workload, args.seed, args.steps, args.warmup)
     print(f"# {args.workload}: {res['us_per_layer_call']:.2f} us/layer-call, "
           f"{res['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
@@ -211,6 +233,7 @@ def main():
             "frac": res["hbm_frac"],
             "traffic": None,
         },
+        "copy_probe_gbps": copy_gbps,
         "cpu_baseline": cpu,
         "detail": res,
         "secondary": secondary,

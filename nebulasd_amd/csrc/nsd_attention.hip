@@ -6,36 +6,61 @@
 // q_len query rows (up to 64) are packed as the N dimension of fp16 MFMAs,
 // so each K/V tile of the segment is read from HBM exactly once:
 //
-//   S^T[token][row] = K[token][:] . Q[row][:]        (A = K, B = Q^T)
+//   S^T[token][row] = K[token][:] . Q[row][:]            (A = K, B = Q^T)
 //   O^T[dim][row]  += V^T[dim][token] . P^T[token][row]  (A = V^T, B = P^T)
 //
-// using v_mfma_f32_16x16x32_f16.  Both products leave a lane holding one
-// query row (lane & 15) of a 16-row tile, so the online softmax state of a
-// row lives in one lane column and needs only two cross-row shuffles.
-// K tiles load straight into the A-operand layout with 16-byte loads; V is
-// loaded 16 bytes per lane and transposed 8x8 (halves) inside groups of 8
-// lanes with three butterfly exchange stages.
+// S^T uses v_mfma_f32_16x16x32_f16 (k = head dim), O^T uses
+// v_mfma_f32_16x16x16_f16 (k = the 16 tokens of one cache block).  Both leave
+// a lane holding one query row (lane & 15) of a 16-row tile, so a row's
+// online-softmax state lives in one lane column, and the S^T result of a
+// block is already the P^T operand of the PV product (lane group g holds
+// tokens 4g..4g+3).
 //
-// Work split.  The host planner cuts the stream of (segment, 32-token chunk)
-// work into equal contiguous ranges, one per workgroup ("worker"); a
-// workgroup's four waves take the chunks of a piece round-robin and merge
-// their softmax states through LDS.  Segments cut across workers write fp32
+// Data path per wave and 16-token block, three blocks in flight:
+//   K : 16-byte global loads straight into the MFMA A layout (registers);
+//   V : coalesced 16-byte global loads -> per-wave LDS staging (rows padded
+//       to 272 B) -> ds_read_b64_tr_b16 transposing reads = V^T A operand;
+//   Q : staged once per piece in LDS, read as the B operand.
+// A three-stage register ring holds the K/V loads of the next blocks; each
+// stage's K is refilled as soon as S^T has consumed it and its V as soon as
+// it is staged, so every wave keeps about two blocks of loads in flight.
+//
+// Work split.  The host planner cuts the stream of (segment, 16-token block)
+// work into equal contiguous ranges, one per workgroup ("worker"); the four
+// waves of a workgroup take a piece's blocks round-robin and merge their
+// softmax states through LDS.  Segments cut across workers write fp32
 // partials (normalised O, log2-sum-exp) that the combine kernel merges.
 //
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB
 //   contiguous at ((blk*L + layer)*Hkv + head)*16*128 (:49-50, :70-71).
+#include <type_traits>
+#include <utility>
+
 #include "nsd_device.h"
+
+#ifndef NSD_T1_STAGES
+#define NSD_T1_STAGES 3
+#define NSD_T1_WAVES 2
+#define NSD_T2_STAGES 3
+#define NSD_T2_WAVES 1
+#endif
 
 namespace nsd {
 namespace {
 
 constexpr int D = kHeadDim;         // 128
 constexpr int BS = kBlockTokens;     // 16
-constexpr int CT = kChunkTokens;     // 32 tokens = two blocks per MFMA step
 constexpr int NW = 4;                // waves per workgroup
+constexpr int ROWB = D * 2 + 16;     // LDS bytes per staged fp16 row (padded: 16 B bank shift)
 constexpr int RS = D + 4;            // LDS row stride (floats) for the wave merge
 constexpr float kLn2 = 0.69314718055994531f;
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 
 struct AttnArgs {
   const f16* q;            // [R, Hq, D]
@@ -45,9 +70,11 @@ struct AttnArgs {
   const f16* v_cache;
   const int32_t* bt;
   int64_t bt_stride;
-  const int32_t* plan;
+  const int32_t* workers;  // plan: worker table
+  const int32_t* pieces;   // plan: piece records
   float* part_o;           // [slots, rows_max, D]
   float* part_lse;         // [slots, rows_max]  (log2 domain)
+  int32_t* counters;       // [combines] arrival counters, zero between calls
   int32_t* status;
   int64_t num_blocks;
   int64_t blk_stride;      // elements per cache block: L*Hkv*16*128
@@ -55,52 +82,11 @@ struct AttnArgs {
   float scale_log2;        // softmax_scale * log2(e)
 };
 
-__device__ inline uint32_t xchg(uint32_t v, int mask) {
-  return (uint32_t)__shfl_xor((int)v, mask, kWave);
-}
-
-// 8x8 transpose of 16-bit elements inside each group of 8 lanes (lane bits
-// 0..2): afterwards lane x, element y holds what lane y, element x held.
-// Element y of a lane lives in dword y>>1, half y&1.  Each stage swaps one
-// lane bit with the matching element bit.
-__device__ inline void transpose8x8_b16(u32x4& d, int lane) {
-  {  // lane bit 2 <-> element bit 2 (dwords {0,1} vs {2,3})
-    const bool b = lane & 4;
-    const uint32_t s0 = b ? d[0] : d[2], s1 = b ? d[1] : d[3];
-    const uint32_t r0 = xchg(s0, 4), r1 = xchg(s1, 4);
-    if (b) { d[0] = r0; d[1] = r1; } else { d[2] = r0; d[3] = r1; }
-  }
-  {  // lane bit 1 <-> element bit 1 (dwords {0,2} vs {1,3})
-    const bool b = lane & 2;
-    const uint32_t s0 = b ? d[0] : d[1], s1 = b ? d[2] : d[3];
-    const uint32_t r0 = xchg(s0, 2), r1 = xchg(s1, 2);
-    if (b) { d[0] = r0; d[2] = r1; } else { d[1] = r0; d[3] = r1; }
-  }
-  {  // lane bit 0 <-> element bit 0 (halves of each dword)
-    const bool b = lane & 1;
-    // lanes with bit 0 clear keep low halves and send high halves; the others the reverse.
-    const uint32_t sel = b ? 0x05040100u : 0x07060302u;
-    const uint32_t s0 = __builtin_amdgcn_perm(d[1], d[0], sel);
-    const uint32_t s1 = __builtin_amdgcn_perm(d[3], d[2], sel);
-    const uint32_t r0 = xchg(s0, 1), r1 = xchg(s1, 1);
-    if (b) {
-      d[0] = __builtin_amdgcn_perm(d[0], r0, 0x07060100u);
-      d[1] = __builtin_amdgcn_perm(d[1], r0, 0x07060302u);
-      d[2] = __builtin_amdgcn_perm(d[2], r1, 0x07060100u);
-      d[3] = __builtin_amdgcn_perm(d[3], r1, 0x07060302u);
-    } else {
-      d[0] = __builtin_amdgcn_perm(r0, d[0], 0x05040100u);
-      d[1] = __builtin_amdgcn_perm(r0, d[1], 0x07060100u);
-      d[2] = __builtin_amdgcn_perm(r1, d[2], 0x05040100u);
-      d[3] = __builtin_amdgcn_perm(r1, d[3], 0x07060100u);
-    }
-  }
-}
-
-__device__ inline f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
-
-__device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+__device__ inline f32x4 mfma_k32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline f32x4 mfma_k16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
 // Worker id of this workgroup: hardware dispatches workgroup i to XCD i % 8,
@@ -111,59 +97,269 @@ __device__ inline int worker_id() {
   return (b & 7) * (nb >> 3) + (b >> 3);
 }
 
+// LDS byte sizes: Q rows, then max(per-wave V staging, two-slot wave merge).
 template <int NT>
-__global__ __launch_bounds__(NW * kWave) void paged_attn_kernel(AttnArgs a) {
-  extern __shared__ float smem[];
-  float* s_acc = smem;                          // [NW-1][NT*16][RS]
-  float* s_m = smem + (NW - 1) * NT * 16 * RS;  // [NW][NT*16]
-  float* s_l = s_m + NW * NT * 16;              // [NW][NT*16]
+constexpr int lds_q_bytes() { return NT * 16 * ROWB; }
+constexpr int lds_v_bytes() { return NW * BS * ROWB; }
+template <int NT>
+constexpr int lds_merge_bytes() { return 2 * NT * 16 * RS * 4 + 2 * 2 * NT * 16 * 4; }
+template <int NT>
+constexpr size_t lds_bytes() {
+  return lds_q_bytes<NT>() +
+         (lds_v_bytes() > lds_merge_bytes<NT>() ? lds_v_bytes() : lds_merge_bytes<NT>());
+}
+
+// Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time unrolled).
+template <int N, typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+// Transposing LDS read: lane j of each 16-lane group receives, in slot m,
+// 16-bit element (j % 4) of the 8 bytes addressed by lane 4*m + j/4.
+__device__ inline f16x4 ds_read_tr16(const lds_char* p) {
+  fp16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)p);
+  return __builtin_bit_cast(f16x4, t);
+}
+
+// Per row-tile count NT: K/V ring depth and the occupancy the registers allow.
+template <int NT> struct Tune;
+template <> struct Tune<1> { static constexpr int stages = NSD_T1_STAGES, waves = NSD_T1_WAVES; };
+template <> struct Tune<2> { static constexpr int stages = NSD_T2_STAGES, waves = NSD_T2_WAVES; };
+template <> struct Tune<3> { static constexpr int stages = 2, waves = 1; };
+template <> struct Tune<4> { static constexpr int stages = 1, waves = 1; };
+
+// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
+// other inside a kernel).  They are written and read with device-scope (sc1)
+// vector accesses through a raw buffer resource, which the L2 keeps coherent
+// without the whole-cache write-back and invalidate of an agent-scope fence.
+constexpr int kDeviceScope = 16;              // cache-policy bit of sc1 on gfx950
+constexpr int kRawBufferConfig = 0x00020000;  // raw 32-bit buffer, no format conversion
+
+__device__ inline __amdgpu_buffer_rsrc_t raw_buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes,
+                                           kRawBufferConfig);
+}
+__device__ inline void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kDeviceScope);
+}
+__device__ inline f32x4 load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDeviceScope));
+}
+
+// Merge the partials of a segment cut across workers (run by the workgroup
+// that wrote the segment's last partial): thread (row, 8 dims), slots folded
+// with a running max (online log-sum-exp), eight slots' loads in flight at a
+// time.  Same exp2-domain combine as phase 2 of the reference
+// (paged_attn.py:128-149).
+__device__ void combine_segment(const AttnArgs& a, int h, int first, int n_slots, int row_start,
+                                int n_rows) {
+  const int d8 = threadIdx.x & 15;
+  const uint32_t sbytes = (uint32_t)a.rows_max * D * 4;  // one slot's O partial
+  const __amdgpu_buffer_rsrc_t ro =
+      raw_buffer(a.part_o + (int64_t)first * a.rows_max * D, (uint32_t)n_slots * sbytes);
+  const float* pl_base = a.part_lse + (int64_t)first * a.rows_max;
+  for (int n = threadIdx.x >> 4; n < n_rows; n += NW * kWave / 16) {
+    const uint32_t off = ((uint32_t)n * D + 8 * d8) * 4;
+    float M = -INFINITY, W = 0.f;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_slots; s0 += 8) {
+      f32x4 v0[8], v1[8];
+      float ls[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sidx = s0 + u < n_slots ? s0 + u : s0;
+        const float l = __hip_atomic_load(pl_base + (int64_t)sidx * a.rows_max + n,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ls[u] = s0 + u < n_slots ? l : -INFINITY;
+        v0[u] = load_coherent(ro, sidx * sbytes + off);
+        v1[u] = load_coherent(ro, sidx * sbytes + off + 16);
+      }
+      float mb = M;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mb = fmaxf(mb, ls[u]);
+      const float scale = exp2f(M - mb);  // M = -inf at start: 0 (acc and W are 0)
+      acc0 *= scale;
+      acc1 *= scale;
+      W *= scale;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wgt = exp2f(ls[u] - mb);
+        acc0 += v0[u] * wgt;
+        acc1 += v1[u] * wgt;
+        W += wgt;
+      }
+      M = mb;
+    }
+    const float inv = 1.f / W;
+    const int qi = n / a.gqa, gh = n - qi * a.gqa;
+    const int64_t orow = (int64_t)(row_start + qi) * a.hq + h * a.gqa + gh;
+    f16x8 hv = {(f16)(acc0[0] * inv), (f16)(acc0[1] * inv), (f16)(acc0[2] * inv),
+                (f16)(acc0[3] * inv), (f16)(acc1[0] * inv), (f16)(acc1[1] * inv),
+                (f16)(acc1[2] * inv), (f16)(acc1[3] * inv)};
+    *reinterpret_cast<f16x8*>(a.o + orow * D + 8 * d8) = hv;
+    if (d8 == 0 && a.lse != nullptr) a.lse[orow] = (M + __log2f(W)) * kLn2;
+  }
+}
+
+// A piece of work as the kernel sees it (one plan record).
+struct Piece {
+  int h, b_begin, b_end, slot, row_start, q_len, ctx, comb, comb_first, comb_slots;
+  int64_t seq_id;
+};
+
+__device__ inline Piece read_piece(const int32_t* r) {
+  Piece p;
+  p.h = r[kPieceHead];
+  p.b_begin = r[kPieceBlkBegin];
+  p.b_end = r[kPieceBlkEnd];
+  p.slot = r[kPieceSlot];
+  p.row_start = r[kPieceRowStart];
+  p.q_len = r[kPieceQLen];
+  p.seq_id = r[kPieceSeqId];
+  p.ctx = r[kPieceCtx];
+  p.comb = r[kPieceComb];
+  p.comb_first = r[kPieceCombFirst];
+  p.comb_slots = r[kPieceCombSlots];
+  return p;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(Tune<NT>::waves)))
+void paged_attn_kernel(AttnArgs a) {
+  constexpr int NSTAGE = Tune<NT>::stages;
+  extern __shared__ __align__(16) char smem_raw[];
+  __shared__ int s_flag;                                  // last-arrival flag of a split segment
+  lds_char* smem = (lds_char*)smem_raw;
+  lds_char* s_q = smem;                                   // [NT*16][ROWB]
+  float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [2][NT*16][RS] (aliases V)
+  float* s_ml = s_acc + 2 * NT * 16 * RS;                 // merge: [2][2][NT*16]
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 15;   // row within a 16-row tile (B/D column)
   const int lg = lane >> 4;   // k-group of the MFMA operands
+  lds_char* s_v = smem + lds_q_bytes<NT>() + wave * BS * ROWB;  // this wave's V staging
+  // transposing-read address of dim tile 0: lane (g, a = lane % 16) points at
+  // token 4g + a/4, dims 4*(a%4) .. +3
+  const lds_char* tr_src = s_v + (4 * lg + (lr >> 2)) * ROWB + 8 * (lr & 3);
 
-  const int32_t* plan = a.plan;
-  const int32_t* groups = plan + plan[kPlanOffGroups];
-  const int32_t* wstart = plan + plan[kPlanOffWorkerStart];
-  const int32_t* pieces = plan + plan[kPlanOffPieces];
-  const int w = worker_id();
-  const int p_begin = wstart[w], p_end = wstart[w + 1];
+  const int32_t* wrow = a.workers + kWorkerWords * worker_id();
+  const int p_begin = wrow[0], p_end = wrow[1];
+  if (p_begin >= p_end) return;  // whole workgroup idle
+
+  // this wave's blocks of a piece: b_begin + wave + NW*k, k < wave_blocks
+  auto wave_blocks = [&](const Piece& p) {
+    const int n = p.b_end - p.b_begin;
+    return n > wave ? (n - wave + NW - 1) / NW : 0;
+  };
+  // Block ids of this wave's blocks k0 .. k0+63 of piece p, one per lane (-1
+  // when out of the pool, flagged).  Read back per block with readlane, so
+  // no per-block load sits in front of the K/V loads.
+  auto load_ids = [&](const Piece& p, int pnk, int k0) -> int {
+    const int kk = k0 + lane;
+    int v = 0;
+    if (kk < pnk) {
+      v = a.bt[p.seq_id * a.bt_stride + p.b_begin + wave + NW * kk];
+      if (v < 0 || v >= a.num_blocks) {
+        flag_status(a.status, NSD_STATUS_BAD_BLOCK);
+        v = -1;
+      }
+    }
+    return v;
+  };
+  // Q rows of piece p (zero padded), 16 B per thread and step.
+  auto load_q = [&](const Piece& p, u32x4 (&qv)[NT]) {
+    const int n_rows = p.q_len * a.gqa;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int u = threadIdx.x + i * NW * kWave;  // 16-byte unit: row u/16, column u%16
+      const int n = u >> 4;
+      qv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (n < n_rows) {
+        const int qi = n / a.gqa, gh = n - qi * a.gqa;
+        qv[i] = *reinterpret_cast<const u32x4*>(
+            a.q + ((int64_t)(p.row_start + qi) * a.hq + p.h * a.gqa + gh) * D + (u & 15) * 8);
+      }
+    }
+  };
+  auto head_base = [&](const f16* cache, const Piece& p) {
+    return cache + ((int64_t)a.layer * a.hkv + p.h) * BS * D;
+  };
+
+  // Ring of in-flight K/V blocks.  A block id < 0 (out of the pool) reads
+  // pool block 0 instead and its scores are masked.
+  f16x8 kr[NSTAGE][4];
+  u32x4 vr[NSTAGE][4];
+  int bid[NSTAGE];
+  auto issue_k = [&](int st, const f16* kb, int id) {
+    const f16* kp = kb + (int64_t)(id < 0 ? 0 : id) * a.blk_stride + lr * D + lg * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kr[st][kk] = *reinterpret_cast<const f16x8*>(kp + kk * 32);
+  };
+  auto issue_v = [&](int st, const f16* vb, int id) {
+    const f16* vp = vb + (int64_t)(id < 0 ? 0 : id) * a.blk_stride + lg * D + lr * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vr[st][i] = *reinterpret_cast<const u32x4*>(vp + 4 * i * D);
+  };
+  // first NSTAGE blocks of piece p into the ring
+  auto issue_first = [&](const Piece& p, int pnk, int pids) {
+    const f16* kb = head_base(a.k_cache, p);
+    const f16* vb = head_base(a.v_cache, p);
+#pragma unroll
+    for (int st = 0; st < NSTAGE; ++st) {
+      bid[st] = -1;
+      if (st < pnk) {
+        bid[st] = __builtin_amdgcn_readlane(pids, st);
+        issue_k(st, kb, bid[st]);
+        issue_v(st, vb, bid[st]);
+      }
+    }
+  };
+
+  Piece cur = read_piece(wrow + kWorkerFirstPiece);
+  int nk = wave_blocks(cur);
+  int ids = load_ids(cur, nk, 0);
+  u32x4 qv[NT];
+  load_q(cur, qv);
+  issue_first(cur, nk, ids);
 
   for (int pc = p_begin; pc < p_end; ++pc) {
-    const int seg = pieces[4 * pc + 0];
-    const int c_begin = pieces[4 * pc + 1];
-    const int c_end = pieces[4 * pc + 2];
-    const int slot = pieces[4 * pc + 3];
-    const int g = seg / a.hkv;
-    const int h = seg - g * a.hkv;
-    const int row_start = groups[4 * g + 0];
-    const int q_len = groups[4 * g + 1];
-    const int64_t seq_id = groups[4 * g + 2];
-    const int ctx = groups[4 * g + 3];
-    const int n_rows = q_len * a.gqa;
-    const int total = ctx + q_len;            // tokens of the segment
-    const int n_blk = (total + BS - 1) / BS;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int u = threadIdx.x + i * NW * kWave;
+      *(lds_u32x4*)(s_q + (u >> 4) * ROWB + (u & 15) * 16) = qv[i];
+    }
+    __syncthreads();
 
-    // Q^T as the B operand: lane (lg, lr) holds row 16j+lr, dims kk*32+lg*8..+8.
-    f16x8 qb[NT][4];
+    // next piece: its record now, its ids and Q during this piece, its first
+    // blocks as soon as this piece's loads are all issued
+    const bool has_next = pc + 1 < p_end;
+    Piece nxt = cur;
+    if (has_next) nxt = read_piece(a.pieces + kPieceWords * (pc + 1));
+    int nxt_nk = 0, nxt_ids = 0;
+    bool prefetched = false;
+    auto prefetch_next = [&]() {
+      nxt_nk = wave_blocks(nxt);
+      nxt_ids = load_ids(nxt, nxt_nk, 0);
+      load_q(nxt, qv);
+      prefetched = true;
+    };
+
+    const int n_rows = cur.q_len * a.gqa;
+    const int total = cur.ctx + cur.q_len;  // tokens of the segment
+    const f16* kbase = head_base(a.k_cache, cur);
+    const f16* vbase = head_base(a.v_cache, cur);
     int sl[NT];  // seq_len of the lane's row (causal bound inside the group)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int n = 16 * j + lr;
-      if (n < n_rows) {
-        const int qi = n / a.gqa, gh = n - qi * a.gqa;
-        const f16* qp = a.q + ((int64_t)(row_start + qi) * a.hq + h * a.gqa + gh) * D + lg * 8;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) qb[j][kk] = *reinterpret_cast<const f16x8*>(qp + kk * 32);
-        sl[j] = ctx + qi + 1;
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) qb[j][kk] = f16x8{};
-        sl[j] = total;
-      }
+      sl[j] = n < n_rows ? cur.ctx + n / a.gqa + 1 : total;
     }
-
     float m[NT], l[NT];
     f32x4 acc[NT][8];
 #pragma unroll
@@ -174,86 +370,48 @@ __global__ __launch_bounds__(NW * kWave) void paged_attn_kernel(AttnArgs a) {
       for (int mt = 0; mt < 8; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int32_t* bt_row = a.bt + seq_id * a.bt_stride;
-    const int64_t head_off = ((int64_t)a.layer * a.hkv + h) * BS * D;
-
-    for (int c = c_begin + wave; c < c_end; c += NW) {
-      // Block ids of the chunk's two 16-token blocks (the second may not exist).
-      int64_t blk[2];
+    // One block of the ring: scores, refill, stage V, softmax, PV.
+    auto step = [&](auto stage, int k) {
+      constexpr int st = decltype(stage)::value;
+      const int blk = cur.b_begin + wave + NW * k;
+      const bool valid = bid[st] >= 0;
+      // S^T: lane (lg, lr) gets scores of row 16j+lr for tokens 16*blk + 4lg + i.
+      f32x4 s[NT];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int bi = 2 * c + tt;
-        int64_t id = -1;
-        if (bi < n_blk) {
-          id = bt_row[bi];
-          if (id < 0 || id >= a.num_blocks) {
-            if (lane == 0) flag_status(a.status, NSD_STATUS_BAD_BLOCK);
-            id = -1;
-          }
+      for (int j = 0; j < NT; ++j) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const f16x8 qb = *(const lds_f16x8*)(s_q + (16 * j + lr) * ROWB + kk * 64 + lg * 16);
+          t = mfma_k32(kr[st][kk], qb, t);
         }
-        blk[tt] = id;
+        s[j] = t;
       }
-
-      // K: A operand, lane (lg, lr) = token lr of block tt, dims kk*32+lg*8..+8.
-      f16x8 ka[2][4];
-      // V: lane (lg, hh = (lane>>3)&1, x = lane&7) loads token T(lg, x) =
-      // (x>>2)*16 + 4*lg + (x&3), dims 16*mt + 8*hh .. +8; after the 8x8
-      // transpose the lane holds dim 16*mt + lr for tokens T(lg, 0..7).
-      u32x4 vr[8];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        if (blk[tt] >= 0) {
-          const f16* kp = a.k_cache + blk[tt] * a.blk_stride + head_off + lr * D + lg * 8;
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) ka[tt][kk] = *reinterpret_cast<const f16x8*>(kp + kk * 32);
-        } else {
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) ka[tt][kk] = f16x8{};
-        }
+      // refill this stage with block k + NSTAGE
+      const int kn = k + NSTAGE;
+      int nid = -1;
+      if (kn < nk) {
+        if ((kn & 63) == 0) ids = load_ids(cur, nk, kn);
+        nid = __builtin_amdgcn_readlane(ids, kn & 63);
+        issue_k(st, kbase, nid);
       }
-      {
-        const int x = lane & 7;
-        const int tt = x >> 2;
-        const int tok = 4 * lg + (x & 3);
-        const int64_t id = blk[tt];
-        if (id >= 0) {
-          const f16* vp = a.v_cache + id * a.blk_stride + head_off + tok * D + 8 * ((lane >> 3) & 1);
+      // stage V row-major (tokens 4i + lg), then refill the V registers
 #pragma unroll
-          for (int mt = 0; mt < 8; ++mt) vr[mt] = *reinterpret_cast<const u32x4*>(vp + 16 * mt);
-        } else {
-#pragma unroll
-          for (int mt = 0; mt < 8; ++mt) vr[mt] = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+      for (int i = 0; i < 4; ++i) *(lds_u32x4*)(s_v + (4 * i + lg) * ROWB + lr * 16) = vr[st][i];
+      if (kn < nk) issue_v(st, vbase, nid);
 
-      // S^T tiles: lane (lg, lr) gets scores of row 16j+lr for tokens
-      // 32c + 16tt + 4lg + i, i = 0..3.
-      f32x4 s[2][NT];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) t = mfma16x16x32(ka[tt][kk], qb[j][kk], t);
-          s[tt][j] = t;
-        }
-
-      // Online softmax in the exp2 domain, one row per lane column.
-      const int t0 = c * CT + 4 * lg;
-      f16x8 pb[NT];
+      // online softmax in the exp2 domain, one row per lane column
+      const int t0 = blk * BS + 4 * lg;
+      f16x4 pb[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         float mx = -INFINITY;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int t = t0 + 16 * tt + i;
-            const float v = t < sl[j] ? s[tt][j][i] * a.scale_log2 : -INFINITY;
-            s[tt][j][i] = v;
-            mx = fmaxf(mx, v);
-          }
+        for (int i = 0; i < 4; ++i) {
+          const float v = (valid && t0 + i < sl[j]) ? s[j][i] * a.scale_log2 : -INFINITY;
+          s[j][i] = v;
+          mx = fmaxf(mx, v);
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         const float m_new = fmaxf(m[j], mx);
@@ -261,27 +419,38 @@ __global__ __launch_bounds__(NW * kWave) void paged_attn_kernel(AttnArgs a) {
         const float alpha = exp2f(m[j] - m_use);
         float psum = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = exp2f(s[tt][j][i] - m_use);
-            psum += p;
-            pb[j][tt * 4 + i] = (f16)p;
-          }
+        for (int i = 0; i < 4; ++i) {
+          const float p = exp2f(s[j][i] - m_use);
+          psum += p;
+          pb[j][i] = (f16)p;
+        }
         l[j] = l[j] * alpha + psum;
         m[j] = m_new;
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) acc[j][mt] *= alpha;
       }
-
-      // O^T += V^T P^T for the 8 dim tiles.
+      // O^T += V^T P^T, one transposing read per 16-dim tile
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
-        transpose8x8_b16(vr[mt], lane);
-        const f16x8 va = as_f16x8(vr[mt]);
+        const f16x4 va = ds_read_tr16(tr_src + 32 * mt);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[j][mt] = mfma16x16x32(va, pb[j], acc[j][mt]);
+        for (int j = 0; j < NT; ++j) acc[j][mt] = mfma_k16(va, pb[j], acc[j][mt]);
       }
+      bid[st] = nid;
+    };
+
+    // Unrolled ring: block k always lives in stage k % NSTAGE.
+    int k = 0;
+    for (; k + NSTAGE <= nk; k += NSTAGE) {
+      static_for<NSTAGE>([&](auto st) { step(st, k + decltype(st)::value); });
+      if (has_next && !prefetched) prefetch_next();
+    }
+    static_for<NSTAGE - 1>([&](auto st) {
+      if (k + decltype(st)::value < nk) step(st, k + decltype(st)::value);
+    });
+    if (has_next) {
+      if (!prefetched) prefetch_next();
+      issue_first(nxt, nxt_nk, nxt_ids);  // in flight during the merge below
     }
 
     // Row sums across the four k-groups.
@@ -291,113 +460,115 @@ __global__ __launch_bounds__(NW * kWave) void paged_attn_kernel(AttnArgs a) {
       l[j] += __shfl_xor(l[j], 32, kWave);
     }
 
-    // Merge the waves' states through LDS (wave 0 finishes the piece).
-    if (lg == 0) {
+    // Merge the four waves' states through LDS in two rounds:
+    // waves 2,3 -> waves 0,1, then wave 1 -> wave 0.
+    __syncthreads();  // every wave is done with its V staging (aliased below)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        s_m[wave * NT * 16 + 16 * j + lr] = m[j];
-        s_l[wave * NT * 16 + 16 * j + lr] = l[j];
+    for (int round = 0; round < 2; ++round) {
+      const int senders = round == 0 ? 2 : 1;  // waves [senders, 2*senders) send
+      if (wave >= senders && wave < 2 * senders) {
+        const int sslot = wave - senders;
+        float* sa = s_acc + sslot * NT * 16 * RS;
+        float* sm = s_ml + sslot * 2 * NT * 16;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt)
+            *reinterpret_cast<f32x4*>(sa + (16 * j + lr) * RS + 16 * mt + 4 * lg) = acc[j][mt];
+          if (lg == 0) {
+            sm[16 * j + lr] = m[j];
+            sm[NT * 16 + 16 * j + lr] = l[j];
+          }
+        }
       }
-    }
-    if (wave > 0) {
+      __syncthreads();
+      if (wave < senders) {
+        const float* sa = s_acc + wave * NT * 16 * RS;
+        const float* sm = s_ml + wave * 2 * NT * 16;
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+        for (int j = 0; j < NT; ++j) {
+          const float mo = sm[16 * j + lr], lo = sm[NT * 16 + 16 * j + lr];
+          const float M = fmaxf(m[j], mo);
+          const float M_use = M == -INFINITY ? 0.f : M;
+          const float fa = exp2f(m[j] - M_use), fb = exp2f(mo - M_use);
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
-          *reinterpret_cast<f32x4*>(s_acc + ((wave - 1) * NT * 16 + 16 * j + lr) * RS + 16 * mt +
-                                    4 * lg) = acc[j][mt];
+          for (int mt = 0; mt < 8; ++mt)
+            acc[j][mt] = acc[j][mt] * fa +
+                         *reinterpret_cast<const f32x4*>(sa + (16 * j + lr) * RS + 16 * mt + 4 * lg) * fb;
+          l[j] = l[j] * fa + lo * fb;
+          m[j] = M;
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
+
     if (wave == 0) {
+      const __amdgpu_buffer_rsrc_t rpart =
+          raw_buffer(a.part_o + (int64_t)(cur.slot < 0 ? 0 : cur.slot) * a.rows_max * D,
+                     (uint32_t)a.rows_max * D * 4);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int n = 16 * j + lr;
-        float mw[NW], M = -INFINITY;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-          mw[ww] = s_m[ww * NT * 16 + n];
-          M = fmaxf(M, mw[ww]);
-        }
-        const float M_use = M == -INFINITY ? 0.f : M;
-        float fw[NW], L = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-          fw[ww] = exp2f(mw[ww] - M_use);
-          L += fw[ww] * s_l[ww * NT * 16 + n];
-        }
+        const float L = l[j];
         const float inv = L > 0.f ? 1.f / L : 0.f;
         const bool live = n < n_rows;
         const int qi = n / a.gqa, gh = n - qi * a.gqa;
-        const int64_t orow = (int64_t)(row_start + qi) * a.hq + h * a.gqa + gh;
+        const int64_t orow = (int64_t)(cur.row_start + qi) * a.hq + cur.h * a.gqa + gh;
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) {
-          f32x4 v = acc[j][mt] * fw[0];
-#pragma unroll
-          for (int ww = 1; ww < NW; ++ww)
-            v += *reinterpret_cast<const f32x4*>(s_acc + ((ww - 1) * NT * 16 + n) * RS + 16 * mt +
-                                                 4 * lg) * fw[ww];
-          v *= inv;
+          const f32x4 v = acc[j][mt] * inv;
           if (live) {
-            if (slot < 0) {
+            if (cur.slot < 0) {
               f16x4 hv = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
               *reinterpret_cast<f16x4*>(a.o + orow * D + 16 * mt + 4 * lg) = hv;
             } else {
-              *reinterpret_cast<f32x4*>(a.part_o + ((int64_t)slot * a.rows_max + n) * D + 16 * mt +
-                                        4 * lg) = v;
+              store_coherent(rpart, ((uint32_t)n * D + 16 * mt + 4 * lg) * 4, v);
             }
           }
         }
         if (live && lg == 0) {
-          const float lse2 = L > 0.f ? M + __log2f(L) : -INFINITY;
-          if (slot < 0) {
+          const float lse2 = L > 0.f ? m[j] + __log2f(L) : -INFINITY;
+          if (cur.slot < 0) {
             if (a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
           } else {
-            a.part_lse[(int64_t)slot * a.rows_max + n] = lse2;
+            __hip_atomic_store(a.part_lse + (int64_t)cur.slot * a.rows_max + n, lse2,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
       }
     }
-    __syncthreads();
-  }
-}
-
-// Merge the partials of segments cut across workers: one workgroup per
-// segment, one thread per (row, dim).  Mirrors phase 2 of the reference
-// (paged_attn.py:128-149) in the same exp2 domain.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  const int32_t* plan = a.plan;
-  const int32_t* groups = plan + plan[kPlanOffGroups];
-  const int32_t* comb = plan + plan[kPlanOffCombines] + 4 * blockIdx.x;
-  const int seg = comb[0], first = comb[1], n_slots = comb[2];
-  const int g = seg / a.hkv, h = seg - g * a.hkv;
-  const int row_start = groups[4 * g + 0];
-  const int n_rows = groups[4 * g + 1] * a.gqa;
-  for (int idx = threadIdx.x; idx < n_rows * D; idx += blockDim.x) {
-    const int n = idx / D, d = idx - n * D;
-    float M = -INFINITY;
-    for (int s = 0; s < n_slots; ++s) M = fmaxf(M, a.part_lse[(int64_t)(first + s) * a.rows_max + n]);
-    const float M_use = M == -INFINITY ? 0.f : M;
-    float wsum = 0.f, acc = 0.f;
-    for (int s = 0; s < n_slots; ++s) {
-      const int64_t ps = (int64_t)(first + s) * a.rows_max + n;
-      const float wgt = exp2f(a.part_lse[ps] - M_use);
-      wsum += wgt;
-      acc += wgt * a.part_o[ps * D + d];
+    // A split segment is finished by the workgroup that writes its last
+    // partial.  Wave 0 waits until its device-scope partial stores are
+    // complete, then counts the arrival; the last arriver merges all of the
+    // segment's partials (read with device-scope loads) and puts the counter
+    // back to zero for the next call.
+    if (cur.slot >= 0) {
+      if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keeps the stores above
+        __builtin_amdgcn_s_waitcnt(0);                           // ... and completed
+        const int old = __hip_atomic_fetch_add(a.counters + cur.comb, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        s_flag = old == cur.comb_slots - 1;
+      }
+      __syncthreads();
+      if (s_flag) {
+        combine_segment(a, cur.h, cur.comb_first, cur.comb_slots, cur.row_start, n_rows);
+        if (threadIdx.x == 0)
+          __hip_atomic_store(a.counters + cur.comb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-    const int qi = n / a.gqa, gh = n - qi * a.gqa;
-    const int64_t orow = (int64_t)(row_start + qi) * a.hq + h * a.gqa + gh;
-    a.o[orow * D + d] = (f16)(acc / wsum);
-    if (d == 0 && a.lse != nullptr) a.lse[orow] = (M + __log2f(wsum)) * kLn2;
+    // The next piece restages Q (s_q is not aliased by the merge area, and
+    // every read of it ended before the merge barriers).
+    if (has_next) {
+      cur = nxt;
+      nk = nxt_nk;
+      ids = nxt_ids;
+    }
   }
 }
 
 template <int NT>
-constexpr size_t lds_bytes() {
-  return sizeof(float) * ((NW - 1) * NT * 16 * RS + 2 * NW * NT * 16);
-}
-
-template <int NT>
-int launch_nt(const AttnArgs& args, int grid, int n_combine, hipStream_t stream) {
+int launch_nt(const AttnArgs& args, int grid, hipStream_t stream) {
   static bool attr_set = false;  // per-process: raise the dynamic-LDS limit once
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_attn_kernel<NT>),
@@ -407,17 +578,9 @@ int launch_nt(const AttnArgs& args, int grid, int n_combine, hipStream_t stream)
       return fail(NSD_ERR_HIP, "paged_attention: LDS attribute: %s", hipGetErrorString(e));
     attr_set = true;
   }
-  if (grid > 0) {
-    hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(NW * kWave), lds_bytes<NT>(),
-                       stream, args);
-    int rc = launch_status("paged_attention");
-    if (rc) return rc;
-  }
-  if (n_combine > 0) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_combine), dim3(256), 0, stream, args);
-    return launch_status("paged_attention combine");
-  }
-  return NSD_OK;
+  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(NW * kWave), lds_bytes<NT>(), stream,
+                     args);
+  return launch_status("paged_attention");
 }
 
 template <int NT>
@@ -463,7 +626,7 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   if (block_size != BS)
     return fail(NSD_ERR_UNSUPPORTED, "paged_attention: block_size=%d (only 16)", block_size);
   if (!plan_host || !plan_dev) return fail(NSD_ERR_INVALID, "paged_attention: null plan");
-  if (plan_host[kPlanMagic] != kPlanMagicValue || plan_host[kPlanVersion] != 1)
+  if (plan_host[kPlanMagic] != kPlanMagicValue || plan_host[kPlanVersion] != kPlanVersionValue)
     return fail(NSD_ERR_INVALID, "paged_attention: not a plan (bad magic/version)");
   if (plan_host[kPlanHq] != num_q_heads || plan_host[kPlanHkv] != num_kv_heads)
     return fail(NSD_ERR_INVALID, "paged_attention: plan built for Hq=%d Hkv=%d, called with %d/%d",
@@ -482,7 +645,8 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   if (rows_max < 1 || rows_max > kMaxGroupRows || grid % 8 != 0)
     return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan header");
   const int64_t n_slots = plan_host[kPlanSlots];
-  const int64_t need = n_slots * rows_max * (int64_t)(D + 1) * 4;
+  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(D + 1) * 4 + 255) / 256 * 256;
+  const int64_t need = n_combine > 0 ? part_bytes + n_combine * 4 : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return fail(NSD_ERR_WORKSPACE, "paged_attention: workspace %lld bytes < %lld needed",
                 (long long)workspace_bytes, (long long)need);
@@ -495,9 +659,11 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   args.v_cache = static_cast<const f16*>(v_cache);
   args.bt = block_table;
   args.bt_stride = bt_stride;
-  args.plan = plan_dev;
+  args.workers = plan_dev + plan_host[kPlanOffWorkers];
+  args.pieces = plan_dev + plan_host[kPlanOffPieces];
   args.part_o = static_cast<float*>(workspace);
   args.part_lse = static_cast<float*>(workspace) + n_slots * rows_max * D;
+  args.counters = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + part_bytes);
   args.status = status;
   args.num_blocks = num_blocks;
   args.blk_stride = (int64_t)num_layers * num_kv_heads * BS * D;
@@ -512,9 +678,9 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   hipStream_t st = as_stream(stream);
   const int nt = (rows_max + 15) / 16;
   switch (nt) {
-    case 1: return launch_nt<1>(args, grid, n_combine, st);
-    case 2: return launch_nt<2>(args, grid, n_combine, st);
-    case 3: return launch_nt<3>(args, grid, n_combine, st);
-    default: return launch_nt<4>(args, grid, n_combine, st);
+    case 1: return launch_nt<1>(args, grid, st);
+    case 2: return launch_nt<2>(args, grid, st);
+    case 3: return launch_nt<3>(args, grid, st);
+    default: return launch_nt<4>(args, grid, st);
   }
 }

@@ -15,10 +15,10 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Plan word layout (int32), shared by the planner and the attention launch.
 enum PlanHeader {
   kPlanMagic = 0,      // 0x4E534450
-  kPlanVersion,        // 1
+  kPlanVersion,        // 2
   kPlanRows,           // decode/verify rows covered
   kPlanGroups,         // verify groups
-  kPlanPieces,         // (segment, chunk range) pieces
+  kPlanPieces,         // (segment, block range) pieces
   kPlanWorkers,        // launch grid (multiple of 8)
   kPlanCombines,       // segments cut into >1 piece
   kPlanSlots,          // partial slots
@@ -26,17 +26,42 @@ enum PlanHeader {
   kPlanHq,
   kPlanHkv,
   kPlanOffGroups,      // word offset of groups [n_groups][4] {row_start, q_len, seq_id, ctx}
-  kPlanOffWorkerStart, // word offset of worker piece starts [n_workers+1]
-  kPlanOffPieces,      // word offset of pieces [n_pieces][4] {segment, chunk_begin, chunk_end, slot}
-  kPlanOffCombines,    // word offset of combines [n_combines][4] {segment, first_slot, n_slots, 0}
+  kPlanOffWorkers,     // word offset of the worker table [n_workers][kWorkerWords]
+  kPlanOffPieces,      // word offset of pieces [n_pieces][kPieceWords]
+  kPlanOffCombines,    // word offset of combines [n_combines][kPieceWords]
   kPlanWords,          // total words
 };
 static_assert(kPlanWords + 1 == NSD_PLAN_HEADER_WORDS, "plan header size");
 
+// A piece: blocks [blk_begin, blk_end) of one (group, kv head) segment, with
+// the group's description inlined so a worker needs one record per piece.
+enum PieceField {
+  kPieceHead = 0,   // kv head
+  kPieceBlkBegin,   // first 16-token block
+  kPieceBlkEnd,     // one past the last block
+  kPieceSlot,       // partial slot, or -1 when the piece is the whole segment
+  kPieceRowStart,   // first decode row of the group
+  kPieceQLen,       // rows in the group
+  kPieceSeqId,      // block-table row
+  kPieceCtx,        // tokens before the group's first new token
+  kPieceComb,       // combine record of the segment, or -1
+  kPieceCombFirst,  // first partial slot of the segment
+  kPieceCombSlots,  // partial slots of the segment
+  kPiecePad,
+  kPieceWords,
+};
+// A worker-table row: {first piece, end piece, <first piece record>, 0, 0},
+// so a workgroup reaches its first piece with a single 64-byte load.
+constexpr int kWorkerWords = 16;
+constexpr int kWorkerFirstPiece = 2;
+// A combine record: {kv head, first slot, slot count, row start, q_len, 0, 0, 0}.
+enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
+
 constexpr int32_t kPlanMagicValue = 0x4E534450;
+constexpr int32_t kPlanVersionValue = 4;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
-constexpr int kChunkTokens = 32;
 constexpr int kMaxGroupRows = 64;
+constexpr int kMaxSlotsPerSegment = 128;
 
 }  // namespace nsd

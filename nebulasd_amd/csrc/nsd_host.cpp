@@ -13,7 +13,8 @@ namespace nsd {
 
 namespace {
 thread_local std::string g_last_error;
-constexpr int64_t kMinChunksPerWorker = 4;  // one 32-token chunk per wave of a workgroup
+constexpr int64_t kMinBlocksPerWorker = 8;  // two 16-token blocks per wave of a workgroup
+constexpr int64_t kPieceCostBlocks = 12;    // fixed cost of a piece, in blocks of streaming
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -40,7 +41,8 @@ extern "C" int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_w
   if (n_rows < 0 || num_kv_heads <= 0 || n_workers <= 0) return -1;
   const int64_t segs = n_rows * num_kv_heads;
   const int64_t nw = round_up8(n_workers);
-  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + (nw + 1) + 4 * (nw + segs) + 4 * segs;
+  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kWorkerWords * nw + kPieceWords * (nw + segs) +
+         kPieceWords * segs;
 }
 
 extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
@@ -92,58 +94,128 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t n_groups = (int64_t)groups.size() / 4;
   const int64_t n_segs = n_groups * num_kv_heads;
 
-  // 2. chunk counts per segment (segment = group * Hkv + kv head).
+  // 2. block counts per segment (segment = group * Hkv + kv head).
   std::vector<int64_t> seg_start(n_segs + 1, 0);
   for (int64_t s = 0; s < n_segs; ++s) {
     const int32_t* g = &groups[4 * (s / num_kv_heads)];
     const int64_t tokens = (int64_t)g[3] + g[1];
-    seg_start[s + 1] = seg_start[s] + (tokens + kChunkTokens - 1) / kChunkTokens;
+    seg_start[s + 1] = seg_start[s] + (tokens + kBlockTokens - 1) / kBlockTokens;
   }
   const int64_t total = seg_start[n_segs];
 
-  // 3. equal contiguous chunk ranges per worker.
-  int64_t active = std::min<int64_t>(n_workers, (total + kMinChunksPerWorker - 1) / kMinChunksPerWorker);
-  const int64_t grid = total > 0 ? round_up8(std::max<int64_t>(active, 1)) : 0;
-  if (total == 0) active = 0;
+  // 3. contiguous block ranges per worker of near-equal cost, where a
+  //    worker's cost is its blocks plus kPieceCostBlocks per piece it opens
+  //    (a piece pays a prologue, a wave merge and an output write).  The
+  //    target cost is the smallest one that fits the stream into the workers;
+  //    it also keeps every segment under kMaxSlotsPerSegment pieces.
+  int64_t max_seg = 0;
+  for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
+  const int64_t cmin = kPieceCostBlocks + std::max<int64_t>(
+      kMinBlocksPerWorker, (max_seg + kMaxSlotsPerSegment - 3) / (kMaxSlotsPerSegment - 2));
+  // Greedy cut of the stream for a per-worker cost cap; returns the workers used
+  // and, if `cuts` is given, each worker's [begin, end) in stream blocks.
+  auto cut_stream = [&](int64_t cap, std::vector<int64_t>* cuts) {
+    int64_t used = 0, pos = 0, seg_i = 0;
+    while (pos < total) {
+      while (seg_start[seg_i + 1] <= pos) ++seg_i;
+      const int64_t begin = pos;
+      int64_t budget = cap - kPieceCostBlocks;
+      while (pos < total && budget > 0) {
+        const int64_t take = std::min(budget, seg_start[seg_i + 1] - pos);
+        pos += take;
+        budget -= take;
+        if (pos == seg_start[seg_i + 1] && pos < total) {
+          ++seg_i;
+          if (budget <= kPieceCostBlocks) break;  // opening another piece would not pay
+          budget -= kPieceCostBlocks;
+        }
+      }
+      if (cuts) cuts->insert(cuts->end(), {begin, pos});
+      ++used;
+    }
+    return used;
+  };
+  const int64_t want = std::max<int64_t>(1, n_workers);
+  int64_t lo = cmin, hi = std::max(cmin, total + kPieceCostBlocks);
+  if (total > 0 && cut_stream(lo, nullptr) > want) {
+    while (lo + 1 < hi) {  // smallest cap that fits in `want` workers
+      const int64_t mid = (lo + hi) / 2;
+      if (cut_stream(mid, nullptr) <= want) hi = mid; else lo = mid;
+    }
+    lo = hi;
+  }
+  std::vector<int64_t> cuts;
+  const int64_t active = total > 0 ? cut_stream(lo, &cuts) : 0;
+  const int64_t grid = total > 0 ? round_up8(active) : 0;
   std::vector<int32_t> wstart(grid + 1, 0);
-  std::vector<int32_t> pieces;  // {segment, chunk_begin, chunk_end, slot}
+  std::vector<int32_t> pieces;  // kPieceWords per piece
   int64_t seg = 0;
   for (int64_t w = 0; w < grid; ++w) {
-    wstart[w] = (int32_t)(pieces.size() / 4);
+    wstart[w] = (int32_t)(pieces.size() / kPieceWords);
     if (w >= active) continue;
-    int64_t a = total * w / active;
-    const int64_t b = total * (w + 1) / active;
+    int64_t a = cuts[2 * w];
+    const int64_t b = cuts[2 * w + 1];
     while (a < b) {
       while (seg_start[seg + 1] <= a) ++seg;
       const int64_t end = std::min(b, seg_start[seg + 1]);
-      pieces.insert(pieces.end(), {(int32_t)seg, (int32_t)(a - seg_start[seg]),
-                                   (int32_t)(end - seg_start[seg]), -1});
+      const int32_t* g = &groups[4 * (seg / num_kv_heads)];
+      pieces.insert(pieces.end(), {(int32_t)(seg % num_kv_heads), (int32_t)(a - seg_start[seg]),
+                                   (int32_t)(end - seg_start[seg]), -1, g[0], g[1], g[2], g[3],
+                                   -1, 0, 0, 0});
       a = end;
     }
   }
-  wstart[grid] = (int32_t)(pieces.size() / 4);
-  const int64_t n_pieces = (int64_t)pieces.size() / 4;
+  wstart[grid] = (int32_t)(pieces.size() / kPieceWords);
+  const int64_t n_pieces = (int64_t)pieces.size() / kPieceWords;
 
   // 4. partial slots for segments cut into several pieces (pieces of one
-  //    segment are adjacent because workers walk the chunk stream in order).
-  std::vector<int32_t> combines;  // {segment, first_slot, n_slots, 0}
+  //    segment are adjacent because workers walk the block stream in order).
+  std::vector<int32_t> combines;  // kPieceWords per record
   int64_t n_slots = 0;
+  auto same_seg = [&](int64_t i, int64_t j) {
+    const int32_t* x = &pieces[kPieceWords * i];
+    const int32_t* y = &pieces[kPieceWords * j];
+    return x[kPieceHead] == y[kPieceHead] && x[kPieceRowStart] == y[kPieceRowStart];
+  };
   for (int64_t i = 0; i < n_pieces;) {
     int64_t j = i + 1;
-    while (j < n_pieces && pieces[4 * j] == pieces[4 * i]) ++j;
+    while (j < n_pieces && same_seg(i, j)) ++j;
+    if (j - i > kMaxSlotsPerSegment)
+      return fail(NSD_ERR_INVALID, "plan: segment cut into %lld pieces", (long long)(j - i));
     if (j - i > 1) {
-      combines.insert(combines.end(), {pieces[4 * i], (int32_t)n_slots, (int32_t)(j - i), 0});
-      for (int64_t k = i; k < j; ++k) pieces[4 * k + 3] = (int32_t)(n_slots++);
+      const int32_t* x = &pieces[kPieceWords * i];
+      const int32_t ci = (int32_t)(combines.size() / kPieceWords);
+      combines.insert(combines.end(), {x[kPieceHead], (int32_t)n_slots, (int32_t)(j - i),
+                                       x[kPieceRowStart], x[kPieceQLen], 0, 0, 0, 0, 0, 0, 0});
+      for (int64_t k = i; k < j; ++k) {
+        int32_t* y = &pieces[kPieceWords * k];
+        y[kPieceSlot] = (int32_t)(n_slots + (k - i));
+        y[kPieceComb] = ci;
+        y[kPieceCombFirst] = (int32_t)n_slots;
+        y[kPieceCombSlots] = (int32_t)(j - i);
+      }
+      n_slots += j - i;
     }
     i = j;
   }
-  const int64_t n_combines = (int64_t)combines.size() / 4;
+  const int64_t n_combines = (int64_t)combines.size() / kPieceWords;
+
+  // 5. worker table: piece range plus an inline copy of the first piece.
+  std::vector<int32_t> wtable(kWorkerWords * grid, 0);
+  for (int64_t w = 0; w < grid; ++w) {
+    int32_t* row = &wtable[kWorkerWords * w];
+    row[0] = wstart[w];
+    row[1] = wstart[w + 1];
+    if (wstart[w] < wstart[w + 1])
+      std::copy(&pieces[kPieceWords * wstart[w]], &pieces[kPieceWords * (wstart[w] + 1)],
+                row + kWorkerFirstPiece);
+  }
 
   const int64_t off_groups = NSD_PLAN_HEADER_WORDS;
   const int64_t off_wstart = off_groups + 4 * n_groups;
-  const int64_t off_pieces = off_wstart + grid + 1;
-  const int64_t off_combines = off_pieces + 4 * n_pieces;
-  const int64_t words = off_combines + 4 * n_combines;
+  const int64_t off_pieces = off_wstart + kWorkerWords * grid;
+  const int64_t off_combines = off_pieces + kPieceWords * n_pieces;
+  const int64_t words = off_combines + kPieceWords * n_combines;
   if (words > plan_capacity)
     return fail(NSD_ERR_WORKSPACE, "plan: needs %lld words, capacity %lld", (long long)words,
                 (long long)plan_capacity);
@@ -152,7 +224,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
 
   int32_t* h = plan;
   h[kPlanMagic] = kPlanMagicValue;
-  h[kPlanVersion] = 1;
+  h[kPlanVersion] = kPlanVersionValue;
   h[kPlanRows] = (int32_t)n_rows;
   h[kPlanGroups] = (int32_t)n_groups;
   h[kPlanPieces] = (int32_t)n_pieces;
@@ -163,17 +235,18 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   h[kPlanHq] = num_q_heads;
   h[kPlanHkv] = num_kv_heads;
   h[kPlanOffGroups] = (int32_t)off_groups;
-  h[kPlanOffWorkerStart] = (int32_t)off_wstart;
+  h[kPlanOffWorkers] = (int32_t)off_wstart;
   h[kPlanOffPieces] = (int32_t)off_pieces;
   h[kPlanOffCombines] = (int32_t)off_combines;
   h[kPlanWords] = (int32_t)words;
   std::copy(groups.begin(), groups.end(), h + off_groups);
-  std::copy(wstart.begin(), wstart.end(), h + off_wstart);
+  std::copy(wtable.begin(), wtable.end(), h + off_wstart);
   std::copy(pieces.begin(), pieces.end(), h + off_pieces);
   std::copy(combines.begin(), combines.end(), h + off_combines);
 
   *plan_words = words;
-  const int64_t part_bytes = n_slots * rows_max * (int64_t)(kHeadDim + 1) * 4;
-  *workspace_bytes = (part_bytes + 255) / 256 * 256;
+  // partial O and log-sum-exp per slot, then one arrival counter per combine
+  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(kHeadDim + 1) * 4 + 255) / 256 * 256;
+  *workspace_bytes = n_combines > 0 ? part_bytes + (n_combines * 4 + 255) / 256 * 256 : 0;
   return NSD_OK;
 }

@@ -6,6 +6,11 @@
 // copies for the cache writes, and wave64 shuffles for the norm reduction.
 #include "nsd_device.h"
 
+// fp32 results are rounded to fp32 and then to fp16, as the reference's
+// `.to(tl.float16)` does; forbid contracting a multiply into a mixed fma
+// that rounds straight to fp16.
+#pragma clang fp contract(off)
+
 namespace nsd {
 namespace {
 

@@ -17,6 +17,8 @@ import numpy as np
 
 from . import _lib
 
+PIECE_WORDS = 12
+WORKER_WORDS = 16
 _workers_cache: dict[tuple[int, int], int] = {}
 
 
@@ -73,9 +75,15 @@ def decode_plan(words: np.ndarray) -> dict:
         "slots": int(h[_lib.PLAN_SLOTS]),
         "rows_max": int(h[_lib.PLAN_ROWS_MAX]),
         "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
-        "worker_start": words[ow:ow + n_workers + 1],
-        "pieces": words[op:op + 4 * n_pieces].reshape(n_pieces, 4),
-        "combines": words[oc:oc + 4 * n_comb].reshape(n_comb, 4),
+        # per worker: {first piece, end piece, <first piece record>, 0...}
+        "workers_table": words[ow:ow + WORKER_WORDS * n_workers].reshape(n_workers, WORKER_WORDS),
+        "worker_start": np.append(words[ow:ow + WORKER_WORDS * n_workers:WORKER_WORDS],
+                                  words[ow + WORKER_WORDS * (n_workers - 1) + 1] if n_workers else 0),
+        # {kv head, blk_begin, blk_end, slot, row_start, q_len, seq_id, ctx,
+        #  combine, combine first slot, combine slots, 0}
+        "pieces": words[op:op + PIECE_WORDS * n_pieces].reshape(n_pieces, PIECE_WORDS),
+        # {kv head, first_slot, n_slots, row_start, q_len, 0 ...}
+        "combines": words[oc:oc + PIECE_WORDS * n_comb].reshape(n_comb, PIECE_WORDS),
     }
 
 
@@ -127,5 +135,7 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
                                block_size, bt_rows, bt_stride,
                                num_workers(rows_max, device.index), max_group_rows)
     dev = torch.from_numpy(words).to(device, non_blocking=False)
-    workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=device)
+    # zeroed: the tail of the workspace holds arrival counters that every
+    # launch leaves at zero (a fresh plan also recovers from an aborted launch)
+    workspace = torch.zeros(max(ws, 256), dtype=torch.uint8, device=device)
     return AttnPlan(words, dev, workspace, ws, num_q_heads, num_kv_heads)

@@ -90,6 +90,32 @@ def test_attention_every_layer_and_deterministic(gpu):
     assert torch.equal(o, o2) and torch.equal(lse, lse2)
 
 
+def test_attention_reused_plan_split_segments(gpu):
+    """One plan and workspace across calls: long contexts cut into many pieces.
+
+    The per-segment arrival counters in the workspace must be back at zero
+    after every call, or the next call would merge too early.
+    """
+    w = make_workload("target_verify", 7, device=gpu, pool_blocks=4096, num_layers=3,
+                      ctxs=[20000, 33, 9000, 1], q_len=5)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)
+    st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, w.q.device)
+    o = torch.empty_like(w.q)
+    lse = torch.empty(w.q.shape[:2], dtype=torch.float32, device=w.q.device)
+    for layer in (2, 0, 1, 2):
+        paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o, lse,
+                        validate=True)
+        torch.cuda.synchronize()
+        plan = st.attn_plan
+        n_comb = int(plan.host[6])
+        assert n_comb > 0, "the long contexts should be split across workgroups"
+        tail = plan.workspace[plan.workspace_bytes - (-(-4 * n_comb // 256) * 256):]
+        assert int(tail.view(torch.int32)[:n_comb].abs().sum()) == 0
+        check_against_oracle(w, layer, o, lse, f"reused plan layer {layer}")
+
+
 def test_attention_closed_form_single_token(gpu):
     """seq_len = 1: the output is V of token 0 and the LSE its score."""
     w = make_workload("target_verify", 5, device=gpu, pool_blocks=64, num_layers=2,

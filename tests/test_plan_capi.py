@@ -86,35 +86,65 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
             assert seq_ids[r + i] == sid and seq_lens[r + i] == ctx + 1 + i
         r += q_len
     assert r == len(seq_lens)
-    # every (segment, chunk) covered exactly once, workers walk the stream in order
-    chunks = [(-(-(int(g[3]) + int(g[1])) // 32)) for g in groups for _ in range(hkv)]
-    covered = [np.zeros(n, int) for n in chunks]
+    # segment = (group, kv head), in stream order; blocks of 16 tokens
+    seg_of = {(int(g[0]), h): i * hkv + h for i, g in enumerate(groups) for h in range(hkv)}
+    nblk = [(-(-(int(g[3]) + int(g[1])) // 16)) for g in groups for _ in range(hkv)]
+    covered = [np.zeros(n, int) for n in nblk]
     last = (-1, -1)
     for w in range(p["workers"]):
         for pc in range(ws[w], ws[w + 1]):
-            seg, cb, ce, slot = (int(x) for x in pieces[pc])
-            assert 0 <= cb < ce <= chunks[seg]
-            assert (seg, cb) > last
-            last = (seg, ce - 1)
-            covered[seg][cb:ce] += 1
+            h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, pad = (
+                int(x) for x in pieces[pc])
+            seg = seg_of[(row_start, h)]
+            g = groups[seg // hkv]
+            assert (q_len, sid, ctx) == (int(g[1]), int(g[2]), int(g[3]))
+            assert 0 <= bb < be <= nblk[seg]
+            assert (seg, bb) > last
+            last = (seg, be - 1)
+            covered[seg][bb:be] += 1
     assert all((c == 1).all() for c in covered)
     # slots exactly for segments cut into several pieces
     per_seg = {}
-    for seg, cb, ce, slot in pieces:
-        per_seg.setdefault(int(seg), []).append(int(slot))
-    combined = {int(c[0]): (int(c[1]), int(c[2])) for c in p["combines"]}
-    for seg, slots in per_seg.items():
+    for pcs in pieces:
+        per_seg.setdefault((int(pcs[4]), int(pcs[0])), []).append(int(pcs[3]))
+    combined = {(int(c[3]), int(c[0])): (int(c[1]), int(c[2])) for c in p["combines"]}
+    for key, slots in per_seg.items():
+        assert len(slots) <= 128
         if len(slots) == 1:
-            assert slots == [-1] and seg not in combined
+            assert slots == [-1] and key not in combined
         else:
-            first, n = combined[seg]
+            first, n = combined[key]
             assert slots == list(range(first, first + n))
-    # near-equal work per active worker
-    work = [sum(int(pieces[pc][2] - pieces[pc][1]) for pc in range(ws[w], ws[w + 1]))
+    # each piece of a split segment names its combine record and slot range
+    for pcs in pieces:
+        comb, cfirst, cslots = int(pcs[8]), int(pcs[9]), int(pcs[10])
+        if int(pcs[3]) < 0:
+            assert (comb, cfirst, cslots) == (-1, 0, 0)
+        else:
+            c = p["combines"][comb]
+            assert (int(c[3]), int(c[0])) == (int(pcs[4]), int(pcs[0]))
+            assert (cfirst, cslots) == (int(c[1]), int(c[2]))
+            assert cfirst <= int(pcs[3]) < cfirst + cslots
+    # the worker table inlines each worker's first piece
+    for w in range(p["workers"]):
+        row = p["workers_table"][w]
+        assert (row[0], row[1]) == (ws[w], ws[w + 1])
+        if ws[w] < ws[w + 1]:
+            assert list(row[2:14]) == list(pieces[ws[w]])
+    # near-equal cost per active worker: blocks + 12 per piece; only the last
+    # active worker may fall short
+    cost = [sum(int(pieces[pc][2] - pieces[pc][1]) + 12 for pc in range(ws[w], ws[w + 1]))
             for w in range(p["workers"])]
-    active = [x for x in work if x > 0]
-    assert max(active) - min(active) <= 1
+    active = [x for x in cost if x > 0]
+    assert max(active) <= max(active[:-1] or active) and max(active) - min(active[:-1] or active) <= 2 * 12 + 1
     assert p["workers"] % 8 == 0
+
+
+def test_plan_caps_pieces_per_segment(lib):
+    # one 32k request over many workers: at most 128 pieces per (group, kv head)
+    p, _ = _plan([0], [32768], workers=100000, stride=4096)
+    check_plan_invariants(p, [0], [32768], 8, 4)
+    assert max(int(c[2]) for c in p["combines"]) <= 128
 
 
 def test_plan_groups_reference_literal_rows(lib):
@@ -147,7 +177,10 @@ def test_plan_invariants_random(lib, seed):
     for hq, hkv in ((32, 8), (16, 8), (8, 8)):
         p, ws = _plan(seq_ids, seq_lens, hq, hkv, workers, bt_rows=100)
         check_plan_invariants(p, seq_ids, seq_lens, hkv, hq // hkv)
-        assert ws >= p["slots"] * p["rows_max"] * 129 * 4
+        # partials (fp32 O + lse per slot row) then one arrival counter per combine
+        part = -(-p["slots"] * p["rows_max"] * 129 * 4 // 256) * 256
+        cnt = -(-4 * len(p["combines"]) // 256) * 256
+        assert ws == (part + cnt if len(p["combines"]) else 0)
 
 
 def test_plan_splits_long_groups(lib):
