@@ -5,9 +5,11 @@ q_len=5, contexts U[256, 4096], 24,576-block pool, fp16) on inputs already
 resident in HBM.  Steps cycle ``cur_layer`` over all 36 layers so the
 ~144 MB per-layer working set cannot stay in the 256 MB Infinity Cache.
 The timed steps are replayed from a HIP graph of one pass over the layers
-(no host launch overhead inside the timed region).  A secondary line
-measures Draft decode (Qwen3-0.6B shape, B=64).  The CPU baseline times the
-numpy oracle on the same inputs on this host's cores.
+(no host launch overhead inside the timed region), timed with HIP events
+on the stream the kernels run on.  The fused prologue (QK-RMSNorm + RoPE +
+KV store) is timed alone and together with the attention.  A secondary
+entry measures Draft decode (Qwen3-0.6B shape, B=64).  The CPU baseline
+times the numpy oracle on the same inputs on this host's cores.
 
 Prints one JSON line (see ``--help``).
 """
@@ -40,13 +42,44 @@ def parse_args():
     return p.parse_args()
 
 
+def _time_graph(fn, stream, reps: int, wreps: int) -> float:
+    """Capture fn() in a HIP graph on `stream`; µs per replay, timed with HIP
+    events recorded on that same stream around `reps` back-to-back replays."""
+    import torch
+
+    fn()  # plans, kernel attributes: everything a capture must not do
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(wreps):
+            graph.replay()
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return start.elapsed_time(end) * 1e3 / reps
+
+
 def measure(name: str, seed: int, steps: int, warmup: int):
-    """Time `steps` layer calls of workload `name`; returns (result dict, workload)."""
+    """Time `steps` layer calls of workload `name`; returns (result dict, workload).
+
+    Three graphs of one pass over all layers are timed: the attention alone
+    (the headline), the fused prologue alone, and prologue + attention as a
+    layer runs them.  The prologue works on copies of q and fresh k/v rows,
+    so the attention inputs of the first graph are never modified.
+    """
     import torch
 
     from nebulasd_amd.config import EngineConfig, ModelConfig
     from nebulasd_amd.infer_state import build_infer_state, rope_cache
-    from nebulasd_amd.kernels import paged_attention
+    from nebulasd_amd.kernels import paged_attention, qk_norm_rope_store
     from nebulasd_amd.workload import make_workload
 
     dev = torch.device("cuda:0")
@@ -57,40 +90,42 @@ def measure(name: str, seed: int, steps: int, warmup: int):
     st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, dev)
     L = mc.num_layers
     o = torch.empty_like(w.q)
+    g = torch.Generator(device=dev).manual_seed(seed + 1000)
+    hkv = mc.num_kv_heads
+    qp = w.q.clone()
+    kn = torch.randn((w.rows, hkv, 128), device=dev, generator=g).half()
+    vn = torch.randn((w.rows, hkv, 128), device=dev, generator=g).half()
+    qw = (torch.rand(128, device=dev, generator=g) + 0.5).half()
+    kw = (torch.rand(128, device=dev, generator=g) + 0.5).half()
 
-    def one_pass():
+    def attn_pass():
         for layer in range(L):
             paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o)
 
-    one_pass()  # builds the plan, sets kernel attributes
-    torch.cuda.synchronize()
+    def prologue_pass():
+        for layer in range(L):
+            qk_norm_rope_store(qp, kn, vn, w.k_cache, w.v_cache, w.block_table, qw, kw, mc, ec,
+                               st, layer, cos, sin)
+
+    def layer_pass():
+        for layer in range(L):
+            qk_norm_rope_store(qp, kn, vn, w.k_cache, w.v_cache, w.block_table, qw, kw, mc, ec,
+                               st, layer, cos, sin)
+            paged_attention(qp, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o)
+
     stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            one_pass()
-    torch.cuda.synchronize()
-    reps = max(1, steps // L)
-    wreps = max(1, warmup // L)
-    for _ in range(wreps):
-        graph.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps, wreps = max(1, steps // L), max(1, warmup // L)
     t0 = time.perf_counter()
-    start.record()
-    for _ in range(reps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
+    us = _time_graph(attn_pass, stream, reps, wreps) / L
     wall = time.perf_counter() - t0
-    n = reps * L
-    us = start.elapsed_time(end) * 1e3 / n
+    us_pro = _time_graph(prologue_pass, stream, reps, wreps) / L
+    us_layer = _time_graph(layer_pass, stream, reps, wreps) / L
     nbytes = w.algorithmic_bytes()
     gbps = nbytes / (us * 1e-6) / 1e9
     plan = st.attn_plan
     res = {
         "workload": name,
-        "steps": n,
+        "steps": reps * L,
         "us_per_layer_call": us,
         "wall_ms": wall * 1e3,
         "algorithmic_bytes": nbytes,
@@ -102,9 +137,30 @@ def measure(name: str, seed: int, steps: int, warmup: int):
         "kv_tokens": w.kv_tokens(),
         "plan_workers": int(plan.host[5]),
         "plan_rows_max": plan.rows_max,
+        "prologue_us": us_pro,
+        "prologue_bytes": w.prologue_bytes(),
+        "prologue_gbps": w.prologue_bytes() / (us_pro * 1e-6) / 1e9,
+        "prologue_plus_attention_us": us_layer,
     }
-    del graph
     return res, w
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per attention launch for `workload`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy
+    calibration), or None when no row matches."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 5 and parts[0] == workload and not line.startswith("#"):
+                try:
+                    return float(parts[4])
+                except ValueError:
+                    return None
+    return None
 
 
 def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
@@ -231,7 +287,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": res["hbm_frac"],
-            "traffic": None,
+            "traffic": traffic_from_profiles(args.workload),
         },
         "copy_probe_gbps": copy_gbps,
         "cpu_baseline": cpu,

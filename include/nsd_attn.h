@@ -127,9 +127,11 @@ int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w
  *     a verify group (rows of speculative.py:75-89); each group is attended
  *     once per KV head with GQA-group x q_len query rows packed together;
  *     max_group_rows = 1 keeps every row its own group;
- *   - the (group, kv head, 32-token chunk) work is cut into n_workers equal
- *     contiguous ranges; a group/head cut across ranges gets fp32 partials
- *     (normalised O and log2-sum-exp) merged by a combine pass.
+ *   - the (group, kv head, 16-token block) stream is cut into n_workers
+ *     contiguous ranges of near-equal cost (blocks plus a fixed charge per
+ *     range piece); a (group, kv head) segment cut across ranges gets fp32
+ *     partials (normalised O and log2-sum-exp), merged inside the same
+ *     launch by the workgroup that writes the segment's last partial.
  * nsd_attn_plan_bound gives an upper bound on the plan size in int32 words.
  * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
  * 0 <= seq_id < bt_rows), writes the plan into `plan` (capacity
@@ -158,7 +160,10 @@ int nsd_attn_num_workers(int max_rows, int* n_workers);
  * softmax-weighted sum of V (fp16 out, fp32 math).  If lse != NULL it also
  * writes ln(sum exp(score)) as fp32 [n_rows, Hq].
  * plan_host / plan_dev: the same plan words on the host and on the device.
- * workspace: device buffer of at least the bytes reported by the plan.
+ * workspace: device buffer of at least the bytes reported by the plan, 16-byte
+ * aligned and ZERO-FILLED before its first use: its tail holds one arrival
+ * counter per split segment, which every call leaves at zero again.  Calls
+ * that share a workspace must be ordered on one stream (never concurrent).
  */
 int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
                         const void* v_cache, int64_t num_blocks, int num_layers, int layer,

@@ -26,10 +26,12 @@
 // it is staged, so every wave keeps about two blocks of loads in flight.
 //
 // Work split.  The host planner cuts the stream of (segment, 16-token block)
-// work into equal contiguous ranges, one per workgroup ("worker"); the four
-// waves of a workgroup take a piece's blocks round-robin and merge their
-// softmax states through LDS.  Segments cut across workers write fp32
-// partials (normalised O, log2-sum-exp) that the combine kernel merges.
+// work into contiguous ranges of near-equal cost, one per workgroup
+// ("worker"); the four waves of a workgroup take a piece's blocks
+// round-robin and merge their softmax states through LDS.  Segments cut
+// across workers write fp32 partials (normalised O, log2-sum-exp); the
+// workgroup that writes a segment's last partial merges them in the same
+// launch.
 //
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB

@@ -10,6 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from ..plan import plan_for
 from ._util import StatusWord, cache_dims, ptr, require, require_cuda, stream_of
 
 
@@ -45,7 +46,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
             raise ValueError("lse must hold num_decoding_seqs * num_q_heads floats")
     if rows == 0:
         return
-    plan = infer_state.get_attn_plan(model_config, engine_config, block_table)
+    plan = plan_for(infer_state, model_config, engine_config, block_table)
     status = StatusWord(q.device) if validate else None
     _lib.call("nsd_paged_attention",
               q.data_ptr(), o.data_ptr(), ptr(lse), k_cache.data_ptr(), v_cache.data_ptr(),

@@ -139,3 +139,35 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
     # launch leaves at zero (a fresh plan also recovers from an aborted launch)
     workspace = torch.zeros(max(ws, 256), dtype=torch.uint8, device=device)
     return AttnPlan(words, dev, workspace, ws, num_q_heads, num_kv_heads)
+
+
+def plan_for(infer_state, model_config, engine_config, block_table) -> AttnPlan:
+    """The attention plan of one forward, for this package's ``LlamaInferState``
+    or for swiftLLM's own (swiftLLM/swiftllm/worker/infer_state.py:4-29).
+
+    A foreign infer state gets the plan attached as an attribute on first use
+    (every layer of the forward then reuses it).  Its decode rows are read
+    from ``seq_ids_list`` / ``decoding_seq_lens_list`` when the caller set
+    them (the host lists model.py:304-341 already holds), otherwise copied
+    from the device tensors once per forward.
+    """
+    getter = getattr(infer_state, "get_attn_plan", None)
+    if getter is not None:
+        return getter(model_config, engine_config, block_table)
+    plan = getattr(infer_state, "nsd_attn_plan", None)
+    if (plan is not None and plan.num_q_heads == model_config.num_q_heads
+            and plan.num_kv_heads == model_config.num_kv_heads):
+        return plan
+    npf = int(infer_state.num_prefill_seqs)
+    sids = getattr(infer_state, "seq_ids_list", None)
+    slens = getattr(infer_state, "decoding_seq_lens_list", None)
+    if sids is None:
+        sids = infer_state.seq_ids[npf:].cpu().tolist()
+    if slens is None:
+        slens = infer_state.decoding_seq_lens.cpu().tolist()
+    plan = build_attn_plan(sids, slens, model_config.num_q_heads, model_config.num_kv_heads,
+                           model_config.head_dim, engine_config.block_size, block_table.shape[0],
+                           block_table.shape[1], block_table.device,
+                           max_group_rows=int(getattr(infer_state, "max_group_rows", 0)))
+    infer_state.nsd_attn_plan = plan
+    return plan

@@ -96,6 +96,18 @@ class Workload:
         bt = sum(math.ceil((c + s.q_len) / s.block_size) for c in self.ctxs) * 4
         return kv + qo + bt + (self.rows * s.num_q_heads * 4 if with_lse else 0)
 
+    def prologue_bytes(self) -> int:
+        """HBM bytes of the fused prologue: q/k/v read, q/k written back in
+        place, k/v written to their cache slots, plus the per-row metadata,
+        block-table entry and RoPE table rows (gamma vectors are negligible)."""
+        s = self.spec
+        d2 = s.head_dim * 2
+        qkv = self.rows * (s.num_q_heads + 2 * s.num_kv_heads) * d2
+        back = self.rows * (s.num_q_heads + s.num_kv_heads) * d2
+        store = self.rows * 2 * s.num_kv_heads * d2
+        meta = self.rows * (4 + 4 + 4 + 2 * s.head_dim)  # seq_id, seq_len, block id, cos+sin rows
+        return qkv + back + store + meta
+
     def flops(self) -> int:
         """2 flops per multiply-add of QK^T and PV over the attended tokens."""
         s = self.spec

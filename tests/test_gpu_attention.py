@@ -116,6 +116,28 @@ def test_attention_reused_plan_split_segments(gpu):
         check_against_oracle(w, layer, o, lse, f"reused plan layer {layer}")
 
 
+def test_attention_reference_style_infer_state(gpu):
+    """A bare object with only the reference infer state's fields works as the
+    drop-in does (the plan is attached on first use and reused)."""
+    import types
+
+    w = make_workload("target_verify", 8, device=gpu, pool_blocks=1024, num_layers=2,
+                      ctxs=[100, 700, 3], q_len=5)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    st = types.SimpleNamespace(
+        num_prefill_seqs=0, num_decoding_seqs=w.rows, softmax_scale=128 ** -0.5,
+        seq_ids=torch.tensor(w.seq_ids, dtype=torch.int32, device=gpu),
+        decoding_seq_lens=torch.tensor(w.seq_lens, dtype=torch.int32, device=gpu))
+    o = torch.empty_like(w.q)
+    lse = torch.empty(w.q.shape[:2], dtype=torch.float32, device=gpu)
+    for layer in (1, 0):
+        paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o, lse)
+        torch.cuda.synchronize()
+        check_against_oracle(w, layer, o, lse, f"reference-style state layer {layer}")
+    assert st.nsd_attn_plan.n_rows == w.rows
+
+
 def test_attention_closed_form_single_token(gpu):
     """seq_len = 1: the output is V of token 0 and the LSE its score."""
     w = make_workload("target_verify", 5, device=gpu, pool_blocks=64, num_layers=2,
