@@ -132,7 +132,11 @@ int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w
  *     range piece); a (group, kv head) segment cut across ranges gets fp32
  *     partials (normalised O and log2-sum-exp), merged inside the same
  *     launch by the workgroup that writes the segment's last partial.
- * nsd_attn_plan_bound gives an upper bound on the plan size in int32 words.
+ * nsd_attn_plan_bound gives the plan size in int32 words for plans that fit
+ * n_workers workers.  A plan may use more workers than asked (each worker
+ * holds at most 32 pieces of at most 512 blocks); when it does not fit
+ * `plan_capacity`, nsd_attn_plan_build returns NSD_ERR_WORKSPACE and sets
+ * *plan_words to the size needed, so the caller can retry.
  * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
  * 0 <= seq_id < bt_rows), writes the plan into `plan` (capacity
  * `plan_capacity` words), and returns its size and the workspace bytes

@@ -15,6 +15,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libnsd_attn.so"
 
 NSD_OK = 0
+NSD_ERR_WORKSPACE = 4
 STATUS_BAD_BLOCK = 1
 STATUS_BAD_SEQ = 2
 STATUS_BAD_POSITION = 4

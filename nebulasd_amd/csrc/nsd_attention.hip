@@ -104,7 +104,7 @@ template <int NT>
 constexpr int lds_q_bytes() { return NT * 16 * ROWB; }
 constexpr int lds_v_bytes() { return NW * BS * ROWB; }
 template <int NT>
-constexpr int lds_merge_bytes() { return 2 * NT * 16 * RS * 4 + 2 * 2 * NT * 16 * 4; }
+constexpr int lds_merge_bytes() { return NW * NT * 16 * RS * 4 + NW * 2 * NT * 16 * 4; }
 template <int NT>
 constexpr size_t lds_bytes() {
   return lds_q_bytes<NT>() +
@@ -230,16 +230,23 @@ __device__ inline Piece read_piece(const int32_t* r) {
   return p;
 }
 
+__device__ inline Piece read_piece_lds(const int32_t* __restrict__ rec_base, int i) {
+  return read_piece(rec_base + kPieceWords * i);
+}
+
 template <int NT>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(Tune<NT>::waves)))
 void paged_attn_kernel(AttnArgs a) {
   constexpr int NSTAGE = Tune<NT>::stages;
+  constexpr int MINB = 2 * NSTAGE;  // blocks per wave and piece, after padding, at least
+  constexpr int kPad = INT32_MIN;   // block id of a padding block (masked, reads block 0)
   extern __shared__ __align__(16) char smem_raw[];
-  __shared__ int s_flag;                                  // last-arrival flag of a split segment
+  __shared__ int s_last[kMaxWorkerPieces];  // piece pc completed its split segment: combine it
+  __shared__ int32_t s_rec[kMaxWorkerPieces * kPieceWords];  // this worker's piece records
   lds_char* smem = (lds_char*)smem_raw;
   lds_char* s_q = smem;                                   // [NT*16][ROWB]
-  float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [2][NT*16][RS] (aliases V)
-  float* s_ml = s_acc + 2 * NT * 16 * RS;                 // merge: [2][2][NT*16]
+  float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [NW][NT*16][RS] (aliases V)
+  float* s_ml = s_acc + NW * NT * 16 * RS;                // merge: [NW][2][NT*16]
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -253,26 +260,33 @@ void paged_attn_kernel(AttnArgs a) {
   const int32_t* wrow = a.workers + kWorkerWords * worker_id();
   const int p_begin = wrow[0], p_end = wrow[1];
   if (p_begin >= p_end) return;  // whole workgroup idle
+  const int n_pc = p_end - p_begin;  // <= kMaxWorkerPieces (checked on the host)
+  for (int i = threadIdx.x; i < n_pc * kPieceWords; i += NW * kWave)
+    s_rec[i] = a.pieces[(int64_t)p_begin * kPieceWords + i];
+  if (threadIdx.x < kMaxWorkerPieces) s_last[threadIdx.x] = 0;
 
-  // this wave's blocks of a piece: b_begin + wave + NW*k, k < wave_blocks
+  // Arrival protocol of split segments.  Each arrival is released by the
+  // wave that made the stores: a segment counts comb_slots * NW arrivals and
+  // whoever brings the last one merges the segment's partials at the end of
+  // its work.  A piece that is not the workgroup's last counts its waves'
+  // arrivals without stalling: each wave adds its arrival once it has
+  // consumed a block whose loads it issued after its partial stores (vector
+  // memory operations of a wave complete in order).
+  int pend_comb = -1, pend_pc = -1, pend_target = 0;  // arrival not yet counted
+  int done_comb = -1, done_pc = -1, done_target = 0, done_old = 0;  // counted, not yet checked
+
+  // This wave's blocks of a piece are b_begin + wave + NW*k, k < wave_blocks;
+  // the wave runs at least MINB and a multiple of NSTAGE blocks per piece,
+  // the extra ones being padding.
   auto wave_blocks = [&](const Piece& p) {
     const int n = p.b_end - p.b_begin;
     return n > wave ? (n - wave + NW - 1) / NW : 0;
   };
-  // Block ids of this wave's blocks k0 .. k0+63 of piece p, one per lane (-1
-  // when out of the pool, flagged).  Read back per block with readlane, so
-  // no per-block load sits in front of the K/V loads.
+  auto padded = [&](int nk) { return nk <= MINB ? MINB : (nk + NSTAGE - 1) / NSTAGE * NSTAGE; };
+  // Raw block ids of this wave's blocks k0 .. k0+63 of piece p, one per lane.
   auto load_ids = [&](const Piece& p, int pnk, int k0) -> int {
     const int kk = k0 + lane;
-    int v = 0;
-    if (kk < pnk) {
-      v = a.bt[p.seq_id * a.bt_stride + p.b_begin + wave + NW * kk];
-      if (v < 0 || v >= a.num_blocks) {
-        flag_status(a.status, NSD_STATUS_BAD_BLOCK);
-        v = -1;
-      }
-    }
-    return v;
+    return kk < pnk ? a.bt[p.seq_id * a.bt_stride + p.b_begin + wave + NW * kk] : kPad;
   };
   // Q rows of piece p (zero padded), 16 B per thread and step.
   auto load_q = [&](const Piece& p, u32x4 (&qv)[NT]) {
@@ -293,69 +307,80 @@ void paged_attn_kernel(AttnArgs a) {
     return cache + ((int64_t)a.layer * a.hkv + p.h) * BS * D;
   };
 
-  // Ring of in-flight K/V blocks.  A block id < 0 (out of the pool) reads
-  // pool block 0 instead and its scores are masked.
+  // Ring of in-flight K/V blocks; block k of a piece lives in stage k % NSTAGE.
+  // Every refill issues its loads (a padding or out-of-pool block reads pool
+  // block 0 and is masked), so the compiler counts the loads in flight
+  // behind each block exactly and never drains the ring early.
+  bool bad_block = false;  // reported once, at the end
   f16x8 kr[NSTAGE][4];
   u32x4 vr[NSTAGE][4];
   int bid[NSTAGE];
-  auto issue_k = [&](int st, const f16* kb, int id) {
-    const f16* kp = kb + (int64_t)(id < 0 ? 0 : id) * a.blk_stride + lr * D + lg * 8;
+  // pool offset of block `id` (padding and bad ids read block 0; bid < 0 masks them)
+  auto block_offset = [&](auto stage, int id) -> int64_t {
+    constexpr int st = decltype(stage)::value;
+    const bool ok = id >= 0 && id < a.num_blocks;
+    bad_block |= !ok && id != kPad;
+    bid[st] = ok ? id : -1;
+    return (int64_t)(ok ? id : 0) * a.blk_stride;
+  };
+  auto issue_k = [&](auto stage, const f16* kb, int64_t off) {
+    constexpr int st = decltype(stage)::value;
+    const f16* kp = kb + off + lr * D + lg * 8;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) kr[st][kk] = *reinterpret_cast<const f16x8*>(kp + kk * 32);
   };
-  auto issue_v = [&](int st, const f16* vb, int id) {
-    const f16* vp = vb + (int64_t)(id < 0 ? 0 : id) * a.blk_stride + lg * D + lr * 8;
+  auto issue_v = [&](auto stage, const f16* vb, int64_t off) {
+    constexpr int st = decltype(stage)::value;
+    const f16* vp = vb + off + lg * D + lr * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) vr[st][i] = *reinterpret_cast<const u32x4*>(vp + 4 * i * D);
   };
-  // first NSTAGE blocks of piece p into the ring
-  auto issue_first = [&](const Piece& p, int pnk, int pids) {
-    const f16* kb = head_base(a.k_cache, p);
-    const f16* vb = head_base(a.v_cache, p);
-#pragma unroll
-    for (int st = 0; st < NSTAGE; ++st) {
-      bid[st] = -1;
-      if (st < pnk) {
-        bid[st] = __builtin_amdgcn_readlane(pids, st);
-        issue_k(st, kb, bid[st]);
-        issue_v(st, vb, bid[st]);
-      }
-    }
+  // id of this wave's block k (< 128) from the two 64-id vectors of a piece
+  auto pick_id = [&](int lo, int hi, int k) {
+    return __builtin_amdgcn_readlane(k < 64 ? lo : hi, k & 63);
   };
 
   Piece cur = read_piece(wrow + kWorkerFirstPiece);
   int nk = wave_blocks(cur);
-  int ids = load_ids(cur, nk, 0);
+  int nkp = padded(nk);
+  int ids_lo = load_ids(cur, nk, 0);
+  int ids_hi = load_ids(cur, nk, 64);
   u32x4 qv[NT];
   load_q(cur, qv);
-  issue_first(cur, nk, ids);
+  const f16* kbase = head_base(a.k_cache, cur);
+  const f16* vbase = head_base(a.v_cache, cur);
+  static_for<NSTAGE>([&](auto st) {
+    constexpr int s = decltype(st)::value;
+    const int64_t off = block_offset(st, s < nk ? pick_id(ids_lo, ids_hi, s) : kPad);
+    issue_k(st, kbase, off);
+    issue_v(st, vbase, off);
+  });
 
-  for (int pc = p_begin; pc < p_end; ++pc) {
+  for (int pc = 0; pc < n_pc; ++pc) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       const int u = threadIdx.x + i * NW * kWave;
       *(lds_u32x4*)(s_q + (u >> 4) * ROWB + (u & 15) * 16) = qv[i];
     }
-    __syncthreads();
+    __syncthreads();  // Q staged (and, the first time, the piece records)
 
-    // next piece: its record now, its ids and Q during this piece, its first
-    // blocks as soon as this piece's loads are all issued
-    const bool has_next = pc + 1 < p_end;
+    // Next piece: record, ids and Q now, its first blocks in this piece's
+    // last group (so the ring runs on across the piece boundary).
+    const bool has_next = pc + 1 < n_pc;
     Piece nxt = cur;
-    if (has_next) nxt = read_piece(a.pieces + kPieceWords * (pc + 1));
-    int nxt_nk = 0, nxt_ids = 0;
-    bool prefetched = false;
-    auto prefetch_next = [&]() {
+    int nxt_nk = 0, nxt_lo = kPad, nxt_hi = kPad;
+    if (has_next) {
+      nxt = read_piece_lds(s_rec, pc + 1);
       nxt_nk = wave_blocks(nxt);
-      nxt_ids = load_ids(nxt, nxt_nk, 0);
+      nxt_lo = load_ids(nxt, nxt_nk, 0);
+      nxt_hi = load_ids(nxt, nxt_nk, 64);
       load_q(nxt, qv);
-      prefetched = true;
-    };
+    }
+    const f16* nxt_kbase = head_base(a.k_cache, nxt);
+    const f16* nxt_vbase = head_base(a.v_cache, nxt);
 
     const int n_rows = cur.q_len * a.gqa;
     const int total = cur.ctx + cur.q_len;  // tokens of the segment
-    const f16* kbase = head_base(a.k_cache, cur);
-    const f16* vbase = head_base(a.v_cache, cur);
     int sl[NT];  // seq_len of the lane's row (causal bound inside the group)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -372,11 +397,12 @@ void paged_attn_kernel(AttnArgs a) {
       for (int mt = 0; mt < 8; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // One block of the ring: scores, refill, stage V, softmax, PV.
-    auto step = [&](auto stage, int k) {
+    // One block: scores, refill the stage, stage V, softmax, PV.  `last`
+    // (compile time): the refill block is in the next piece.
+    auto step = [&](auto stage, auto last, int k) {
       constexpr int st = decltype(stage)::value;
+      constexpr bool kLast = decltype(last)::value;
       const int blk = cur.b_begin + wave + NW * k;
-      const bool valid = bid[st] >= 0;
       // S^T: lane (lg, lr) gets scores of row 16j+lr for tokens 16*blk + 4lg + i.
       f32x4 s[NT];
 #pragma unroll
@@ -389,18 +415,39 @@ void paged_attn_kernel(AttnArgs a) {
         }
         s[j] = t;
       }
-      // refill this stage with block k + NSTAGE
-      const int kn = k + NSTAGE;
-      int nid = -1;
-      if (kn < nk) {
-        if ((kn & 63) == 0) ids = load_ids(cur, nk, kn);
-        nid = __builtin_amdgcn_readlane(ids, kn & 63);
-        issue_k(st, kbase, nid);
+      if constexpr (st == 0) {
+        if (pend_comb >= 0 && k == NSTAGE) {
+          // block NSTAGE of this piece was loaded after the previous piece's
+          // partial stores: once its K is here, so are they
+          asm volatile("" ::"v"(kr[0][0]) : "memory");
+          done_old = 0;
+          if (lane == 0)
+            done_old = __hip_atomic_fetch_add(a.counters + pend_comb, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+          done_comb = pend_comb;
+          done_pc = pend_pc;
+          done_target = pend_target;
+          pend_comb = -1;
+        }
       }
-      // stage V row-major (tokens 4i + lg), then refill the V registers
+      // refill this stage with block k + NSTAGE of this piece or the next:
+      // K now, V once this block's V is staged in LDS (tokens 4i + lg)
+      const int kn = k + NSTAGE;
+      const f16* kb_n = kLast ? nxt_kbase : kbase;
+      const f16* vb_n = kLast ? nxt_vbase : vbase;
+      int id_n;
+      if constexpr (!kLast) {
+        id_n = kn < nk ? pick_id(ids_lo, ids_hi, kn) : kPad;
+      } else {
+        const int jn = kn - nkp;
+        id_n = has_next && jn < nxt_nk ? __builtin_amdgcn_readlane(nxt_lo, jn) : kPad;
+      }
+      const bool valid = bid[st] >= 0;
+      const int64_t off_n = block_offset(stage, id_n);
+      issue_k(stage, kb_n, off_n);
 #pragma unroll
       for (int i = 0; i < 4; ++i) *(lds_u32x4*)(s_v + (4 * i + lg) * ROWB + lr * 16) = vr[st][i];
-      if (kn < nk) issue_v(st, vbase, nid);
+      issue_v(stage, vb_n, off_n);
 
       // online softmax in the exp2 domain, one row per lane column
       const int t0 = blk * BS + 4 * lg;
@@ -438,22 +485,16 @@ void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[j][mt] = mfma_k16(va, pb[j], acc[j][mt]);
       }
-      bid[st] = nid;
     };
 
-    // Unrolled ring: block k always lives in stage k % NSTAGE.
+    // Groups whose refills stay in this piece (at least one: nkp >= 2*NSTAGE),
+    // then the last group, whose refills start the next piece.
     int k = 0;
-    for (; k + NSTAGE <= nk; k += NSTAGE) {
-      static_for<NSTAGE>([&](auto st) { step(st, k + decltype(st)::value); });
-      if (has_next && !prefetched) prefetch_next();
-    }
-    static_for<NSTAGE - 1>([&](auto st) {
-      if (k + decltype(st)::value < nk) step(st, k + decltype(st)::value);
-    });
-    if (has_next) {
-      if (!prefetched) prefetch_next();
-      issue_first(nxt, nxt_nk, nxt_ids);  // in flight during the merge below
-    }
+    do {
+      static_for<NSTAGE>([&](auto st) { step(st, std::false_type{}, k + decltype(st)::value); });
+      k += NSTAGE;
+    } while (k + NSTAGE < nkp);
+    static_for<NSTAGE>([&](auto st) { step(st, std::true_type{}, k + decltype(st)::value); });
 
     // Row sums across the four k-groups.
 #pragma unroll
@@ -462,111 +503,114 @@ void paged_attn_kernel(AttnArgs a) {
       l[j] += __shfl_xor(l[j], 32, kWave);
     }
 
-    // Merge the four waves' states through LDS in two rounds:
-    // waves 2,3 -> waves 0,1, then wave 1 -> wave 0.
+    // Merge the four waves' states in one round: every wave writes its
+    // live rows (acc, m, l) to LDS, then all threads combine them, four dims
+    // per thread and step, and write the fp16 output (or the fp32 partial).
     __syncthreads();  // every wave is done with its V staging (aliased below)
-#pragma unroll
-    for (int round = 0; round < 2; ++round) {
-      const int senders = round == 0 ? 2 : 1;  // waves [senders, 2*senders) send
-      if (wave >= senders && wave < 2 * senders) {
-        const int sslot = wave - senders;
-        float* sa = s_acc + sslot * NT * 16 * RS;
-        float* sm = s_ml + sslot * 2 * NT * 16;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-#pragma unroll
-          for (int mt = 0; mt < 8; ++mt)
-            *reinterpret_cast<f32x4*>(sa + (16 * j + lr) * RS + 16 * mt + 4 * lg) = acc[j][mt];
-          if (lg == 0) {
-            sm[16 * j + lr] = m[j];
-            sm[NT * 16 + 16 * j + lr] = l[j];
-          }
-        }
-      }
-      __syncthreads();
-      if (wave < senders) {
-        const float* sa = s_acc + wave * NT * 16 * RS;
-        const float* sm = s_ml + wave * 2 * NT * 16;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const float mo = sm[16 * j + lr], lo = sm[NT * 16 + 16 * j + lr];
-          const float M = fmaxf(m[j], mo);
-          const float M_use = M == -INFINITY ? 0.f : M;
-          const float fa = exp2f(m[j] - M_use), fb = exp2f(mo - M_use);
-#pragma unroll
-          for (int mt = 0; mt < 8; ++mt)
-            acc[j][mt] = acc[j][mt] * fa +
-                         *reinterpret_cast<const f32x4*>(sa + (16 * j + lr) * RS + 16 * mt + 4 * lg) * fb;
-          l[j] = l[j] * fa + lo * fb;
-          m[j] = M;
-        }
-      }
-      __syncthreads();
-    }
-
-    if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t rpart =
-          raw_buffer(a.part_o + (int64_t)(cur.slot < 0 ? 0 : cur.slot) * a.rows_max * D,
-                     (uint32_t)a.rows_max * D * 4);
+    {
+      float* ma = s_acc + wave * NT * 16 * RS;
+      float* mm = s_ml + wave * 2 * NT * 16;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int n = 16 * j + lr;
-        const float L = l[j];
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        const bool live = n < n_rows;
-        const int qi = n / a.gqa, gh = n - qi * a.gqa;
-        const int64_t orow = (int64_t)(cur.row_start + qi) * a.hq + cur.h * a.gqa + gh;
+        if (n < n_rows) {
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt) {
-          const f32x4 v = acc[j][mt] * inv;
-          if (live) {
-            if (cur.slot < 0) {
-              f16x4 hv = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-              *reinterpret_cast<f16x4*>(a.o + orow * D + 16 * mt + 4 * lg) = hv;
-            } else {
-              store_coherent(rpart, ((uint32_t)n * D + 16 * mt + 4 * lg) * 4, v);
-            }
-          }
-        }
-        if (live && lg == 0) {
-          const float lse2 = L > 0.f ? m[j] + __log2f(L) : -INFINITY;
-          if (cur.slot < 0) {
-            if (a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
-          } else {
-            __hip_atomic_store(a.part_lse + (int64_t)cur.slot * a.rows_max + n, lse2,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int mt = 0; mt < 8; ++mt)
+            *reinterpret_cast<f32x4*>(ma + n * RS + 16 * mt + 4 * lg) = acc[j][mt];
+          if (lg == 0) {
+            mm[n] = m[j];
+            mm[NT * 16 + n] = l[j];
           }
         }
       }
     }
-    // A split segment is finished by the workgroup that writes its last
-    // partial.  Wave 0 waits until its device-scope partial stores are
-    // complete, then counts the arrival; the last arriver merges all of the
-    // segment's partials (read with device-scope loads) and puts the counter
-    // back to zero for the next call.
+    __syncthreads();
+    {
+      const __amdgpu_buffer_rsrc_t rpart =
+          raw_buffer(a.part_o + (int64_t)(cur.slot < 0 ? 0 : cur.slot) * a.rows_max * D,
+                     (uint32_t)a.rows_max * D * 4);
+      for (int idx = threadIdx.x; idx < n_rows * (D / 4); idx += NW * kWave) {
+        const int n = idx / (D / 4), c4 = idx % (D / 4);
+        float mw[NW], lw[NW], M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          mw[w] = s_ml[w * 2 * NT * 16 + n];
+          lw[w] = s_ml[w * 2 * NT * 16 + NT * 16 + n];
+          M = fmaxf(M, mw[w]);
+        }
+        const float M_use = M == -INFINITY ? 0.f : M;
+        f32x4 ov = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float f = exp2f(mw[w] - M_use);
+          L += lw[w] * f;
+          ov += *reinterpret_cast<const f32x4*>(s_acc + (w * NT * 16 + n) * RS + 4 * c4) * f;
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        ov *= inv;
+        const int qi = n / a.gqa, gh = n - qi * a.gqa;
+        const int64_t orow = (int64_t)(cur.row_start + qi) * a.hq + cur.h * a.gqa + gh;
+        const float lse2 = L > 0.f ? M + __log2f(L) : -INFINITY;
+        if (cur.slot < 0) {
+          f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
+          *reinterpret_cast<f16x4*>(a.o + orow * D + 4 * c4) = hv;
+          if (c4 == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
+        } else {
+          store_coherent(rpart, ((uint32_t)n * D + 4 * c4) * 4, ov);
+          if (c4 == 0)
+            __hip_atomic_store(a.part_lse + (int64_t)cur.slot * a.rows_max + n, lse2,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    // Arrivals of split segments (see above).  The previous piece's arrival
+    // was counted during this piece: note whether it was the last one.
+    if (done_comb >= 0) {
+      if (lane == 0 && done_old == done_target - 1) s_last[done_pc] = 1;
+      done_comb = -1;
+    }
     if (cur.slot >= 0) {
-      if (threadIdx.x == 0) {
+      const int target = cur.comb_slots * NW;
+      if (has_next) {
+        pend_comb = cur.comb;
+        pend_pc = pc;
+        pend_target = target;
+      } else {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keeps the stores above
         __builtin_amdgcn_s_waitcnt(0);                           // ... and completed
-        const int old = __hip_atomic_fetch_add(a.counters + cur.comb, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_flag = old == cur.comb_slots - 1;
-      }
-      __syncthreads();
-      if (s_flag) {
-        combine_segment(a, cur.h, cur.comb_first, cur.comb_slots, cur.row_start, n_rows);
-        if (threadIdx.x == 0)
-          __hip_atomic_store(a.counters + cur.comb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          const int old = __hip_atomic_fetch_add(a.counters + cur.comb, NW, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+          if (old == target - NW) s_last[pc] = 1;
+        }
       }
     }
     // The next piece restages Q (s_q is not aliased by the merge area, and
-    // every read of it ended before the merge barriers).
+    // every read of it ended before the merge barriers); its first blocks
+    // are already in the ring.
     if (has_next) {
       cur = nxt;
       nk = nxt_nk;
-      ids = nxt_ids;
+      nkp = padded(nk);
+      ids_lo = nxt_lo;
+      ids_hi = nxt_hi;
+      kbase = nxt_kbase;
+      vbase = nxt_vbase;
     }
   }
+  // Merge the segments whose last arrival this workgroup brought.
+  __syncthreads();
+  for (int pc = 0; pc < n_pc; ++pc) {
+    if (s_last[pc]) {
+      const Piece p = read_piece_lds(s_rec, pc);
+      combine_segment(a, p.h, p.comb_first, p.comb_slots, p.row_start, p.q_len * a.gqa);
+      if (threadIdx.x == 0)
+        __hip_atomic_store(a.counters + p.comb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (bad_block) flag_status(a.status, NSD_STATUS_BAD_BLOCK);
 }
 
 template <int NT>
@@ -646,6 +690,21 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
     return fail(NSD_ERR_INVALID, "paged_attention: q/o/caches must be 16-byte aligned");
   if (rows_max < 1 || rows_max > kMaxGroupRows || grid % 8 != 0)
     return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan header");
+  // the kernel keeps a worker's piece records in LDS and two 64-id vectors
+  // per wave and piece: enforce the planner's limits on this plan
+  const int32_t* wt = plan_host + plan_host[kPlanOffWorkers];
+  const int32_t* pr = plan_host + plan_host[kPlanOffPieces];
+  for (int w = 0; w < grid; ++w) {
+    const int32_t* row = wt + kWorkerWords * w;
+    if (row[1] - row[0] > kMaxWorkerPieces || row[0] < 0 || row[1] > plan_host[kPlanPieces])
+      return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (worker %d)", w);
+  }
+  for (int i = 0; i < plan_host[kPlanPieces]; ++i) {
+    const int32_t* r = pr + kPieceWords * i;
+    if (r[kPieceBlkEnd] - r[kPieceBlkBegin] > kMaxPieceBlocks || r[kPieceBlkBegin] < 0 ||
+        r[kPieceBlkEnd] <= r[kPieceBlkBegin])
+      return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (piece %d)", i);
+  }
   const int64_t n_slots = plan_host[kPlanSlots];
   const int64_t part_bytes = (n_slots * rows_max * (int64_t)(D + 1) * 4 + 255) / 256 * 256;
   const int64_t need = n_combine > 0 ? part_bytes + n_combine * 4 : 0;

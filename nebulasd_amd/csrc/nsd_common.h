@@ -58,10 +58,12 @@ constexpr int kWorkerFirstPiece = 2;
 enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
 
 constexpr int32_t kPlanMagicValue = 0x4E534450;
-constexpr int32_t kPlanVersionValue = 4;
+constexpr int32_t kPlanVersionValue = 5;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
 constexpr int kMaxGroupRows = 64;
 constexpr int kMaxSlotsPerSegment = 128;
+constexpr int kMaxWorkerPieces = 32;   // pieces one workgroup keeps records of
+constexpr int kMaxPieceBlocks = 512;   // 128 blocks per wave: two 64-id vectors
 
 }  // namespace nsd

@@ -13,8 +13,12 @@ namespace nsd {
 
 namespace {
 thread_local std::string g_last_error;
-constexpr int64_t kMinBlocksPerWorker = 8;  // two 16-token blocks per wave of a workgroup
-constexpr int64_t kPieceCostBlocks = 12;    // fixed cost of a piece, in blocks of streaming
+// Cost model of the planner, in 16-token blocks of streaming: a piece costs
+// its blocks (at least kMinPieceBlocks: a wave pads its share of a piece to
+// two ring lengths with masked blocks) plus a fixed kPieceCostBlocks for the
+// wave merge and output write at its end.
+constexpr int64_t kMinPieceBlocks = 24;
+constexpr int64_t kPieceCostBlocks = 8;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -103,34 +107,35 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   }
   const int64_t total = seg_start[n_segs];
 
-  // 3. contiguous block ranges per worker of near-equal cost, where a
-  //    worker's cost is its blocks plus kPieceCostBlocks per piece it opens
-  //    (a piece pays a prologue, a wave merge and an output write).  The
-  //    target cost is the smallest one that fits the stream into the workers;
-  //    it also keeps every segment under kMaxSlotsPerSegment pieces.
+  // 3. contiguous block ranges per worker of near-equal cost (the cost model
+  //    above).  The target cost is the smallest one that fits the stream into
+  //    the workers; it also keeps every segment under kMaxSlotsPerSegment
+  //    pieces, every piece under kMaxPieceBlocks blocks and every worker
+  //    under kMaxWorkerPieces pieces.
   int64_t max_seg = 0;
   for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
   const int64_t cmin = kPieceCostBlocks + std::max<int64_t>(
-      kMinBlocksPerWorker, (max_seg + kMaxSlotsPerSegment - 3) / (kMaxSlotsPerSegment - 2));
+      kMinPieceBlocks, (max_seg + kMaxSlotsPerSegment - 3) / (kMaxSlotsPerSegment - 2));
   // Greedy cut of the stream for a per-worker cost cap; returns the workers used
-  // and, if `cuts` is given, each worker's [begin, end) in stream blocks.
+  // and, if `cuts` is given, each worker's piece boundaries.
   auto cut_stream = [&](int64_t cap, std::vector<int64_t>* cuts) {
     int64_t used = 0, pos = 0, seg_i = 0;
     while (pos < total) {
-      while (seg_start[seg_i + 1] <= pos) ++seg_i;
-      const int64_t begin = pos;
-      int64_t budget = cap - kPieceCostBlocks;
-      while (pos < total && budget > 0) {
-        const int64_t take = std::min(budget, seg_start[seg_i + 1] - pos);
+      int64_t budget = cap;
+      int opened = 0;
+      if (cuts) cuts->push_back(-1);  // worker marker
+      while (pos < total && opened < kMaxWorkerPieces) {
+        while (seg_start[seg_i + 1] <= pos) ++seg_i;
+        if (opened > 0 && budget <= kPieceCostBlocks + kMinPieceBlocks / 2) break;
+        const int64_t take = std::max<int64_t>(
+            1, std::min({budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos,
+                         (int64_t)kMaxPieceBlocks}));
+        if (cuts) cuts->insert(cuts->end(), {pos, pos + take});
         pos += take;
-        budget -= take;
-        if (pos == seg_start[seg_i + 1] && pos < total) {
-          ++seg_i;
-          if (budget <= kPieceCostBlocks) break;  // opening another piece would not pay
-          budget -= kPieceCostBlocks;
-        }
+        budget -= kPieceCostBlocks + std::max(take, kMinPieceBlocks);
+        ++opened;
+        if (budget <= 0) break;
       }
-      if (cuts) cuts->insert(cuts->end(), {begin, pos});
       ++used;
     }
     return used;
@@ -149,22 +154,22 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t grid = total > 0 ? round_up8(active) : 0;
   std::vector<int32_t> wstart(grid + 1, 0);
   std::vector<int32_t> pieces;  // kPieceWords per piece
-  int64_t seg = 0;
-  for (int64_t w = 0; w < grid; ++w) {
-    wstart[w] = (int32_t)(pieces.size() / kPieceWords);
-    if (w >= active) continue;
-    int64_t a = cuts[2 * w];
-    const int64_t b = cuts[2 * w + 1];
-    while (a < b) {
-      while (seg_start[seg + 1] <= a) ++seg;
-      const int64_t end = std::min(b, seg_start[seg + 1]);
-      const int32_t* g = &groups[4 * (seg / num_kv_heads)];
-      pieces.insert(pieces.end(), {(int32_t)(seg % num_kv_heads), (int32_t)(a - seg_start[seg]),
-                                   (int32_t)(end - seg_start[seg]), -1, g[0], g[1], g[2], g[3],
-                                   -1, 0, 0, 0});
-      a = end;
+  int64_t seg = 0, w = -1;
+  for (size_t c = 0; c < cuts.size();) {
+    if (cuts[c] < 0) {  // next worker
+      wstart[++w] = (int32_t)(pieces.size() / kPieceWords);
+      ++c;
+      continue;
     }
+    const int64_t a = cuts[c], b = cuts[c + 1];
+    c += 2;
+    while (seg_start[seg + 1] <= a) ++seg;
+    const int32_t* g = &groups[4 * (seg / num_kv_heads)];
+    pieces.insert(pieces.end(), {(int32_t)(seg % num_kv_heads), (int32_t)(a - seg_start[seg]),
+                                 (int32_t)(b - seg_start[seg]), -1, g[0], g[1], g[2], g[3],
+                                 -1, 0, 0, 0});
   }
+  for (int64_t v = w + 1; v < grid; ++v) wstart[v] = (int32_t)(pieces.size() / kPieceWords);
   wstart[grid] = (int32_t)(pieces.size() / kPieceWords);
   const int64_t n_pieces = (int64_t)pieces.size() / kPieceWords;
 
@@ -216,9 +221,11 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t off_pieces = off_wstart + kWorkerWords * grid;
   const int64_t off_combines = off_pieces + kPieceWords * n_pieces;
   const int64_t words = off_combines + kPieceWords * n_combines;
-  if (words > plan_capacity)
+  if (words > plan_capacity) {
+    *plan_words = words;  // so the caller can retry with a large enough buffer
     return fail(NSD_ERR_WORKSPACE, "plan: needs %lld words, capacity %lld", (long long)words,
                 (long long)plan_capacity);
+  }
   if (words > INT32_MAX || n_slots > INT32_MAX / kMaxGroupRows)
     return fail(NSD_ERR_INVALID, "plan: too large (%lld words)", (long long)words);
 

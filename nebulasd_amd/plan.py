@@ -50,16 +50,21 @@ def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim:
     if cap < 0:
         raise ValueError(f"bad plan bound arguments (rows={len(sid)}, hkv={num_kv_heads}, "
                          f"workers={n_workers})")
-    buf = np.zeros(cap, dtype=np.int32)
-    words = ctypes.c_int64(0)
-    ws = ctypes.c_int64(0)
     i32p = ctypes.POINTER(ctypes.c_int32)
-    _lib.check(lib.nsd_attn_plan_build(
-        sid.ctypes.data_as(i32p), sl.ctypes.data_as(i32p), len(sid), num_q_heads, num_kv_heads,
-        head_dim, block_size, bt_rows, bt_stride, n_workers, max_group_rows,
-        buf.ctypes.data_as(i32p), cap, ctypes.byref(words), ctypes.byref(ws)),
-        "nsd_attn_plan_build")
-    return buf[: words.value].copy(), int(ws.value)
+    for _ in range(2):  # the bound assumes n_workers; a plan that needs more reports its size
+        buf = np.zeros(cap, dtype=np.int32)
+        words = ctypes.c_int64(0)
+        ws = ctypes.c_int64(0)
+        rc = lib.nsd_attn_plan_build(
+            sid.ctypes.data_as(i32p), sl.ctypes.data_as(i32p), len(sid), num_q_heads,
+            num_kv_heads, head_dim, block_size, bt_rows, bt_stride, n_workers, max_group_rows,
+            buf.ctypes.data_as(i32p), cap, ctypes.byref(words), ctypes.byref(ws))
+        if rc == _lib.NSD_ERR_WORKSPACE and words.value > cap:
+            cap = words.value
+            continue
+        _lib.check(rc, "nsd_attn_plan_build")
+        return buf[: words.value].copy(), int(ws.value)
+    raise _lib.NativeLibraryError("nsd_attn_plan_build: plan size did not converge")
 
 
 def decode_plan(words: np.ndarray) -> dict:

@@ -68,6 +68,10 @@ def test_error_paths_without_gpu(lib):
     assert rc == 1 and "not a plan" in _lib.last_error()
 
 
+# planner constants (nebulasd_amd/csrc/nsd_common.h, nsd_host.cpp)
+MAX_WORKER_PIECES, MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, PIECE_COST = 32, 512, 24, 8
+
+
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
     from nebulasd_amd.plan import decode_plan, plan_words
 
@@ -131,12 +135,19 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
         assert (row[0], row[1]) == (ws[w], ws[w + 1])
         if ws[w] < ws[w + 1]:
             assert list(row[2:14]) == list(pieces[ws[w]])
-    # near-equal cost per active worker: blocks + 12 per piece; only the last
-    # active worker may fall short
-    cost = [sum(int(pieces[pc][2] - pieces[pc][1]) + 12 for pc in range(ws[w], ws[w + 1]))
-            for w in range(p["workers"])]
-    active = [x for x in cost if x > 0]
-    assert max(active) <= max(active[:-1] or active) and max(active) - min(active[:-1] or active) <= 2 * 12 + 1
+    # planner limits: pieces per worker, blocks per piece
+    for w in range(p["workers"]):
+        assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES
+    assert all(0 < int(pc[2] - pc[1]) <= MAX_PIECE_BLOCKS for pc in pieces)
+    # near-equal cost per active worker: max(blocks, 24) + 8 per piece; only
+    # the last active worker, or one stopped by the piece limit, may fall short
+    cost = [sum(max(int(pieces[pc][2] - pieces[pc][1]), MIN_PIECE_BLOCKS) + PIECE_COST
+                for pc in range(ws[w], ws[w + 1])) for w in range(p["workers"])]
+    active = [w for w in range(p["workers"]) if cost[w] > 0]
+    top = max(cost[w] for w in active)
+    for w in active[:-1]:
+        assert cost[w] >= top - 2 * (PIECE_COST + MIN_PIECE_BLOCKS) or \
+            ws[w + 1] - ws[w] == MAX_WORKER_PIECES, (w, cost[w], top)
     assert p["workers"] % 8 == 0
 
 
@@ -250,3 +261,16 @@ def test_qwen3_shape_constants():
         (g["num_q_heads"], g["num_kv_heads"], g["hidden_size"], g["head_dim"], g["vocab_size"])
     assert cfg.rope_theta == g["rope_theta"] and cfg.rms_norm_eps == g["rms_norm_eps"]
     assert cfg.has_qk_norm
+
+
+def test_plan_respects_kernel_limits(lib):
+    # thousands of one-block segments: at most 32 pieces per worker, so the
+    # plan grows past the requested 8 workers
+    n = 2000
+    p, _ = _plan(list(range(n)), [1] * n, hq=16, hkv=8, workers=8, bt_rows=n, stride=16)
+    check_plan_invariants(p, list(range(n)), [1] * n, 8, 2)
+    assert p["workers"] > 8
+    # one long request on one worker: pieces of at most 512 blocks
+    p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
+    check_plan_invariants(p, [0], [16 * 4000], 8, 4)
+    assert max(int(c[2]) for c in p["combines"]) <= 128
