@@ -44,8 +44,8 @@
 #ifndef NSD_T1_STAGES
 #define NSD_T1_STAGES 3
 #define NSD_T1_WAVES 2
-#define NSD_T2_STAGES 3
-#define NSD_T2_WAVES 1
+#define NSD_T2_STAGES 2
+#define NSD_T2_WAVES 2
 #endif
 
 namespace nsd {
@@ -404,13 +404,16 @@ void paged_attn_kernel(AttnArgs a) {
       constexpr bool kLast = decltype(last)::value;
       const int blk = cur.b_begin + wave + NW * k;
       // S^T: lane (lg, lr) gets scores of row 16j+lr for tokens 16*blk + 4lg + i.
+      // (Q is re-read from LDS every block rather than held in registers.)
+      const lds_char* qrow = s_q + lr * ROWB + lg * 16;
+      asm volatile("" : "+v"(qrow));
       f32x4 s[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const f16x8 qb = *(const lds_f16x8*)(s_q + (16 * j + lr) * ROWB + kk * 64 + lg * 16);
+          const f16x8 qb = *(const lds_f16x8*)(qrow + 16 * j * ROWB + kk * 64);
           t = mfma_k32(kr[st][kk], qb, t);
         }
         s[j] = t;
