@@ -111,8 +111,10 @@ def test_attention_reused_plan_split_segments(gpu):
         plan = st.attn_plan
         n_comb = int(plan.host[6])
         assert n_comb > 0, "the long contexts should be split across workgroups"
-        tail = plan.workspace[plan.workspace_bytes - (-(-4 * n_comb // 256) * 256):]
-        assert int(tail.view(torch.int32)[:n_comb].abs().sum()) == 0
+        # workspace: partials, then the arrival counters (256-byte aligned parts)
+        part = -(-int(plan.host[7]) * plan.rows_max * 129 * 4 // 256) * 256
+        counters = plan.workspace[part:part + 4 * n_comb].view(torch.int32)
+        assert int(counters.abs().sum()) == 0
         check_against_oracle(w, layer, o, lse, f"reused plan layer {layer}")
 
 
