@@ -1,0 +1,285 @@
+"""Single-GPU speculative decoding loop on random-init Qwen3 models.
+
+This drives the attention path the way NebulaSD's swiftLLM backend does, at
+real model shapes, so that every layer call of a speculative run goes through
+this package's gfx950 kernels:
+
+* decode / verify rows: QK-RMSNorm + RoPE + KV store in one launch
+  (``qk_norm_rope_store``), then paged attention, in the order of
+  swiftLLM/swiftllm/worker/layers/transformer_layer.py:105-185;
+* prefill: ``rmsnorm_inplace`` on q/k, ``rotary_embedding_inplace`` and the
+  prefill ``store_kvcache``, with per-request causal SDPA for the prompt's
+  attention (transformer_layer.py:7-32);
+* the rest of the layer (projections, MLP, norms, lm_head) is plain torch, as
+  in the reference (kernels/linear.py:3-12); weights are random (no
+  checkpoints are available offline).
+
+The loop is NebulaSD's linear speculation: the draft proposes ``depth``
+tokens with single-token decode steps (nebulasd workers/draft/backend.py:52-70);
+the target verifies anchor + proposal as q_len = depth+1 rows
+(workers/target/backend.py:101-127, swiftLLM/swiftllm/speculative.py:75-89);
+greedy acceptance (speculative.py:122-156) appends the accepted proposal and
+the target's bonus token.  When a whole proposal is accepted the draft has not
+seen its last token; its next step then runs that token and the new anchor as
+one two-row group (the reconcile of workers/draft/inputs.py:59-85).
+
+Every ``check_every``-th forward of either model hands one mid-depth attention
+layer call (q, o, LSE, rows) to the caller's ``make_check`` callback; the tests
+compare those calls with the numpy oracle (tests/spec_checks.py,
+tests/run_spec_loop.py for the full 512-request configuration).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import time
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
+from .infer_state import build_infer_state, rope_cache
+from .kernels import (paged_attention, qk_norm_rope_store, rmsnorm_inplace,
+                      rotary_embedding_inplace, store_kvcache)
+from .speculative import compute_greedy_acceptance
+
+
+class RandomQwen3:
+    """A random-init Qwen3 decoder with a paged KV cache of its own."""
+
+    def __init__(self, cfg: dict, seq_blocks: list, device, seed: int, std: float = 0.02):
+        self.mc = mc = ModelConfig(cfg)
+        self.dev = dev = torch.device(device)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        H, I, V = mc.hidden_size, mc.ffn_inter_dim, mc.vocab_size
+        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+
+        def w(*shape, scale=std):
+            return (torch.randn(shape, device=dev, generator=g) * scale).half()
+
+        self.embed = w(V, H, scale=1.0)
+        self.lm_head = w(V, H)
+        self.final_norm = (torch.rand(H, device=dev, generator=g) + 0.5).half()
+        self.layers = []
+        for _ in range(mc.num_layers):
+            self.layers.append(dict(
+                wq=w(hq * d, H), wk=w(hkv * d, H), wv=w(hkv * d, H), wo=w(H, hq * d),
+                wg=w(I, H), wu=w(I, H), wd=w(H, I),
+                n_in=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                n_post=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                q_norm=(torch.rand(d, device=dev, generator=g) + 0.5).half(),
+                k_norm=(torch.rand(d, device=dev, generator=g) + 0.5).half()))
+        # one block-table row per sequence: its blocks drawn from a shuffled pool
+        n_blocks = sum(seq_blocks)
+        perm = torch.randperm(n_blocks, generator=torch.Generator().manual_seed(seed))
+        width = max(seq_blocks)
+        bt = torch.zeros((len(seq_blocks), width), dtype=torch.int32)
+        pos = 0
+        for r, nb in enumerate(seq_blocks):
+            bt[r, :nb] = perm[pos:pos + nb].to(torch.int32)
+            pos += nb
+        self.block_table = bt.to(dev)
+        self.ec = EngineConfig(block_size=16, max_blocks_per_seq=width, num_gpu_blocks=n_blocks)
+        shape = (n_blocks, mc.num_layers, hkv, 16, d)
+        self.k_cache = torch.zeros(shape, dtype=torch.float16, device=dev)
+        self.v_cache = torch.zeros(shape, dtype=torch.float16, device=dev)
+        self.cos, self.sin = rope_cache(d, mc.rope_theta, width * 16 + 1, dev)
+        self.check = None  # (layer, callback) of a sampled attention check
+
+    def _norm(self, x, wgt):
+        return F.rms_norm(x.float(), (x.shape[-1],), wgt.float(), self.mc.rms_norm_eps).half()
+
+    def _mlp(self, lw, x):
+        h = self._norm(x, lw["n_post"])
+        return x + F.linear(F.silu(F.linear(h, lw["wg"])) * F.linear(h, lw["wu"]), lw["wd"])
+
+    def prefill(self, seq_ids: list, prompts: list) -> list:
+        """Run the prompts; returns each one's greedy next token."""
+        mc, dev = self.mc, self.dev
+        lens = [len(p) for p in prompts]
+        st = build_infer_state(seq_ids, [], lens, mc, self.cos, self.sin, dev)
+        x = self.embed[torch.tensor([t for p in prompts for t in p], device=dev)]
+        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+        starts = np.cumsum([0] + lens)
+        for li, lw in enumerate(self.layers):
+            h = self._norm(x, lw["n_in"])
+            q = F.linear(h, lw["wq"]).view(-1, hq, d)
+            k = F.linear(h, lw["wk"]).view(-1, hkv, d)
+            v = F.linear(h, lw["wv"]).view(-1, hkv, d)
+            rmsnorm_inplace(q.view(-1, d), lw["q_norm"], mc.rms_norm_eps)
+            rmsnorm_inplace(k.view(-1, d), lw["k_norm"], mc.rms_norm_eps)
+            rotary_embedding_inplace(q, k, st)
+            store_kvcache(k, v, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st, li)
+            o = torch.empty_like(q)
+            for r in range(len(prompts)):
+                s, e = int(starts[r]), int(starts[r + 1])
+                qr = q[s:e].transpose(0, 1).contiguous()
+                kr = k[s:e].repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
+                vr = v[s:e].repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
+                o[s:e] = F.scaled_dot_product_attention(qr, kr, vr, is_causal=True).transpose(0, 1)
+            x = x + F.linear(o.view(x.shape[0], -1), lw["wo"])
+            x = self._mlp(lw, x)
+        last = torch.tensor(starts[1:] - 1, device=dev)
+        logits = F.linear(self._norm(x[last], self.final_norm), self.lm_head)
+        return logits.argmax(-1).tolist()
+
+    def decode(self, seq_ids: list, seq_lens: list, tokens: list) -> list:
+        """Decode / verify rows (rows of one sequence contiguous, seq_lens
+        rising by one); returns the greedy next token of every row."""
+        mc, dev = self.mc, self.dev
+        st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
+        x = self.embed[torch.tensor(tokens, device=dev)]
+        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+        for li, lw in enumerate(self.layers):
+            h = self._norm(x, lw["n_in"])
+            q = F.linear(h, lw["wq"]).view(-1, hq, d)
+            k = F.linear(h, lw["wk"]).view(-1, hkv, d)
+            v = F.linear(h, lw["wv"]).view(-1, hkv, d)
+            qk_norm_rope_store(q, k, v, self.k_cache, self.v_cache, self.block_table,
+                               lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin)
+            o = torch.empty_like(q)
+            if self.check is not None and self.check[0] == li:
+                lse = torch.empty((q.shape[0], hq), dtype=torch.float32, device=dev)
+                paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
+                                li, o, lse)
+                self.check[1](self, li, q, o, lse, seq_ids, seq_lens)
+                self.check = None
+            else:
+                paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
+                                li, o)
+            x = x + F.linear(o.view(x.shape[0], -1), lw["wo"])
+            x = self._mlp(lw, x)
+        logits = F.linear(self._norm(x, self.final_norm), self.lm_head)
+        return logits.argmax(-1).tolist()
+
+
+def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
+        target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
+        draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, log=None) -> dict:
+    """The speculative loop over `n_requests` synthetic requests; returns a summary.
+
+    With ``check_every`` > 0, every check_every-th forward calls
+    ``make_check()(model, layer, q, o, lse, seq_ids, seq_lens)`` for its
+    mid-depth attention layer call.
+    """
+    dev = torch.device(device)
+    rng = np.random.default_rng(seed)
+    vocab = target_cfg["vocab_size"]
+    plens = rng.integers(prompt_lo, prompt_hi + 1, n_requests).tolist()
+    prompts = [rng.integers(0, vocab, n).tolist() for n in plens]
+    # room for the prompt, the output and one proposal beyond it
+    blocks = [math.ceil((p + new_tokens + depth + 2) / 16) for p in plens]
+    target = RandomQwen3(target_cfg, blocks, dev, seed + 1)
+    draft = RandomQwen3(draft_cfg, blocks, dev, seed + 2)
+    n_checks = 0
+    t0 = time.perf_counter()
+
+    out = [[] for _ in range(n_requests)]
+    chunk = 16
+    for s in range(0, n_requests, chunk):
+        ids = list(range(s, min(n_requests, s + chunk)))
+        first = target.prefill(ids, [prompts[r] for r in ids])
+        draft.prefill(ids, [prompts[r] for r in ids])
+        for r, t in zip(ids, first):
+            out[r].append(t)
+        if log and (s // chunk) % 8 == 7:
+            log(f"prefill: {ids[-1] + 1} of {n_requests} requests")
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    # tokens of the output each cache holds: the target all but the anchor;
+    # the draft the same, or one fewer after a fully accepted proposal
+    draft_missing = [None] * n_requests  # accepted proposal token the draft has not run
+    stats = {"target_forwards": 0, "draft_forwards": 0, "rounds": 0, "proposed": 0,
+             "accepted": 0}
+    step = 0
+    while True:
+        live = [r for r in range(n_requests) if len(out[r]) < new_tokens]
+        if not live:
+            break
+        stats["rounds"] += 1
+        for ds in range(0, len(live), draft_batch):
+            dgroup = live[ds:ds + draft_batch]
+            # draft: `depth` proposals per request
+            props = {r: [] for r in dgroup}
+            for j in range(depth):
+                sids, slens, toks, last_row = [], [], [], {}
+                for r in dgroup:
+                    base = plens[r] + len(out[r]) - 1 + j  # tokens before this step's input
+                    if j == 0 and draft_missing[r] is not None:
+                        sids += [r, r]
+                        slens += [base, base + 1]
+                        toks += [draft_missing[r], out[r][-1]]
+                    else:
+                        sids.append(r)
+                        slens.append(base + 1)
+                        toks.append(out[r][-1] if j == 0 else props[r][-1])
+                    last_row[r] = len(toks) - 1
+                if check_every and make_check and step % check_every == 0:
+                    draft.check = (draft.mc.num_layers // 2, make_check())
+                    n_checks += 1
+                step += 1
+                nxt = draft.decode(sids, slens, toks)
+                stats["draft_forwards"] += 1
+                for r in dgroup:
+                    props[r].append(nxt[last_row[r]])
+                    if j == 0:
+                        draft_missing[r] = None
+            # target: verify each target batch
+            for ts in range(0, len(dgroup), target_batch):
+                tgroup = dgroup[ts:ts + target_batch]
+                sids, slens, toks = [], [], []
+                for r in tgroup:
+                    base = plens[r] + len(out[r]) - 1
+                    rows = [out[r][-1], *props[r]]
+                    sids += [r] * len(rows)
+                    slens += list(range(base + 1, base + 1 + len(rows)))
+                    toks += rows
+                if check_every and make_check and step % check_every == 0:
+                    target.check = (target.mc.num_layers // 2, make_check())
+                    n_checks += 1
+                step += 1
+                post = target.decode(sids, slens, toks)
+                stats["target_forwards"] += 1
+                for i, r in enumerate(tgroup):
+                    p = post[i * (depth + 1):(i + 1) * (depth + 1)]
+                    acc, n_acc = compute_greedy_acceptance(props[r], p, new_tokens - len(out[r]))
+                    stats["proposed"] += depth
+                    stats["accepted"] += n_acc
+                    if n_acc == depth and len(acc) == depth + 1:
+                        draft_missing[r] = props[r][-1]
+                    out[r] += acc
+        if log:
+            log(f"round {stats['rounds']}: {sum(min(len(o), new_tokens) for o in out)} tokens")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    generated = sum(len(o) for o in out)
+    return {
+        "requests": n_requests, "new_tokens": new_tokens, "generated_tokens": generated,
+        "prompt_tokens": int(sum(plens)), "wall_s": wall, "prefill_s": t_prefill,
+        "decode_tokens_per_s": (generated - n_requests) / max(wall - t_prefill, 1e-9),
+        "acceptance_rate": stats["accepted"] / max(stats["proposed"], 1), **stats,
+        "attention_checks": n_checks,
+    }
+
+
+def main():
+    p = argparse.ArgumentParser(description="Speculative loop on random-init Qwen3-0.6B / Qwen3-8B")
+    p.add_argument("--requests", type=int, default=512)
+    p.add_argument("--prompt-lo", type=int, default=128)
+    p.add_argument("--prompt-hi", type=int, default=1024)
+    p.add_argument("--new-tokens", type=int, default=128)
+    p.add_argument("--draft-batch", type=int, default=64)
+    p.add_argument("--target-batch", type=int, default=16)
+    p.add_argument("--depth", type=int, default=4)
+    p.add_argument("--seed", type=int, default=0)
+    a = p.parse_args()
+    res = run(a.requests, a.prompt_lo, a.prompt_hi, a.new_tokens, a.draft_batch, a.target_batch,
+              a.depth, a.seed, log=lambda m: print(m, flush=True))
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
