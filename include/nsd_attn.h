@@ -40,7 +40,7 @@ extern "C" {
 #define NSD_STATUS_BAD_SEQ 2       /* seq_id outside [0, bt_rows) or position outside the row */
 #define NSD_STATUS_BAD_POSITION 4  /* RoPE position outside the cos/sin table */
 
-#define NSD_PLAN_HEADER_WORDS 16
+#define NSD_PLAN_HEADER_WORDS 20
 
 /* Library version (major*10000 + minor*100 + patch). */
 int nsd_version(void);
@@ -129,14 +129,15 @@ int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w
  *     max_group_rows = 1 keeps every row its own group;
  *   - the (group, kv head, 16-token block) stream is cut into n_workers
  *     contiguous ranges of near-equal cost (blocks plus a fixed charge per
- *     range piece); a (group, kv head) segment cut across ranges gets fp32
- *     partials (normalised O and log2-sum-exp), merged inside the same
+ *     range piece), one per workgroup, whose waves claim the range's blocks
+ *     a few at a time; a (group, kv head) segment cut across ranges gets
+ *     fp32 partials (normalised O and log2-sum-exp), merged inside the same
  *     launch by the workgroup that writes the segment's last partial.
  * nsd_attn_plan_bound gives the plan size in int32 words for plans that fit
  * n_workers workers.  A plan may use more workers than asked (each worker
- * holds at most 32 pieces of at most 512 blocks); when it does not fit
- * `plan_capacity`, nsd_attn_plan_build returns NSD_ERR_WORKSPACE and sets
- * *plan_words to the size needed, so the caller can retry.
+ * holds at most 32 pieces); when it does not fit `plan_capacity`,
+ * nsd_attn_plan_build returns NSD_ERR_WORKSPACE and sets *plan_words to the
+ * size needed, so the caller can retry.
  * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
  * 0 <= seq_id < bt_rows), writes the plan into `plan` (capacity
  * `plan_capacity` words), and returns its size and the workspace bytes

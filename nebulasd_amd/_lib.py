@@ -19,12 +19,12 @@ NSD_ERR_WORKSPACE = 4
 STATUS_BAD_BLOCK = 1
 STATUS_BAD_SEQ = 2
 STATUS_BAD_POSITION = 4
-PLAN_HEADER_WORDS = 16
+PLAN_HEADER_WORDS = 20
 
 # Plan header word indices (nsd_common.h, enum PlanHeader).
 PLAN_MAGIC, PLAN_VERSION, PLAN_ROWS, PLAN_GROUPS, PLAN_PIECES, PLAN_WORKERS, PLAN_COMBINES, \
     PLAN_SLOTS, PLAN_ROWS_MAX, PLAN_HQ, PLAN_HKV, PLAN_OFF_GROUPS, PLAN_OFF_WSTART, \
-    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS = range(16)
+    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_STRIDE, PLAN_RING_STAGES = range(18)
 
 _I32P = POINTER(c_int32)
 

@@ -27,8 +27,10 @@
 //
 // Work split.  The host planner cuts the stream of (segment, 16-token block)
 // work into contiguous ranges of near-equal cost, one per workgroup
-// ("worker"); the four waves of a workgroup take a piece's blocks
-// round-robin and merge their softmax states through LDS.  Segments cut
+// ("worker"), and there is one workgroup per compute unit.  The workgroup's
+// waves claim its range a group of ring-depth blocks at a time from a
+// counter in LDS, so a wave that streams faster takes more groups, and merge
+// their softmax states through LDS at the end of each piece.  Segments cut
 // across workers write fp32 partials (normalised O, log2-sum-exp); the
 // workgroup that writes a segment's last partial merges them in the same
 // launch.
@@ -41,19 +43,11 @@
 
 #include "nsd_device.h"
 
-#ifndef NSD_T1_STAGES
-#define NSD_T1_STAGES 3
-#define NSD_T1_WAVES 2
-#define NSD_T2_STAGES 2
-#define NSD_T2_WAVES 2
-#endif
-
 namespace nsd {
 namespace {
 
 constexpr int D = kHeadDim;         // 128
 constexpr int BS = kBlockTokens;     // 16
-constexpr int NW = 4;                // waves per workgroup
 constexpr int ROWB = D * 2 + 16;     // LDS bytes per staged fp16 row (padded: 16 B bank shift)
 constexpr int RS = D + 4;            // LDS row stride (floats) for the wave merge
 constexpr float kLn2 = 0.69314718055994531f;
@@ -81,6 +75,7 @@ struct AttnArgs {
   int64_t num_blocks;
   int64_t blk_stride;      // elements per cache block: L*Hkv*16*128
   int num_layers, layer, hq, hkv, gqa, rows_max;
+  int piece_stride;        // plan: piece records per worker
   float scale_log2;        // softmax_scale * log2(e)
 };
 
@@ -99,16 +94,30 @@ __device__ inline int worker_id() {
   return (b & 7) * (nb >> 3) + (b >> 3);
 }
 
-// LDS byte sizes: Q rows, then max(per-wave V staging, two-slot wave merge).
+// Per row-tile count NT: K/V ring depth (= blocks per claimed group) and
+// waves per workgroup, shared with the planner.
+template <int NT>
+struct Tune {
+  static constexpr int stages = ring_stages(NT);
+  static constexpr int waves = attn_waves(NT);
+};
+
+// LDS byte sizes: Q rows, then max(per-wave V staging, one-round wave merge).
 template <int NT>
 constexpr int lds_q_bytes() { return NT * 16 * ROWB; }
-constexpr int lds_v_bytes() { return NW * BS * ROWB; }
 template <int NT>
-constexpr int lds_merge_bytes() { return NW * NT * 16 * RS * 4 + NW * 2 * NT * 16 * 4; }
+constexpr int lds_v_bytes() { return Tune<NT>::waves * BS * ROWB; }
+template <int NT>
+constexpr int lds_merge_bytes() { return Tune<NT>::waves * NT * 16 * (RS + 2) * 4; }
+// At least half the LDS of a compute unit, so that one workgroup holds a
+// compute unit: its waves then share the unit's work through the claims.
+constexpr int kLdsHalfCu = 80 * 1024 + 16;
 template <int NT>
 constexpr size_t lds_bytes() {
-  return lds_q_bytes<NT>() +
-         (lds_v_bytes() > lds_merge_bytes<NT>() ? lds_v_bytes() : lds_merge_bytes<NT>());
+  const int need = lds_q_bytes<NT>() + (lds_v_bytes<NT>() > lds_merge_bytes<NT>()
+                                            ? lds_v_bytes<NT>()
+                                            : lds_merge_bytes<NT>());
+  return need > kLdsHalfCu ? need : kLdsHalfCu;
 }
 
 // Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time unrolled).
@@ -127,13 +136,6 @@ __device__ inline f16x4 ds_read_tr16(const lds_char* p) {
   fp16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)p);
   return __builtin_bit_cast(f16x4, t);
 }
-
-// Per row-tile count NT: K/V ring depth and the occupancy the registers allow.
-template <int NT> struct Tune;
-template <> struct Tune<1> { static constexpr int stages = NSD_T1_STAGES, waves = NSD_T1_WAVES; };
-template <> struct Tune<2> { static constexpr int stages = NSD_T2_STAGES, waves = NSD_T2_WAVES; };
-template <> struct Tune<3> { static constexpr int stages = 2, waves = 1; };
-template <> struct Tune<4> { static constexpr int stages = 1, waves = 1; };
 
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
 // other inside a kernel).  They are written and read with device-scope (sc1)
@@ -165,7 +167,7 @@ __device__ void combine_segment(const AttnArgs& a, int h, int first, int n_slots
   const __amdgpu_buffer_rsrc_t ro =
       raw_buffer(a.part_o + (int64_t)first * a.rows_max * D, (uint32_t)n_slots * sbytes);
   const float* pl_base = a.part_lse + (int64_t)first * a.rows_max;
-  for (int n = threadIdx.x >> 4; n < n_rows; n += NW * kWave / 16) {
+  for (int n = threadIdx.x >> 4; n < n_rows; n += blockDim.x / 16) {
     const uint32_t off = ((uint32_t)n * D + 8 * d8) * 4;
     float M = -INFINITY, W = 0.f;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -208,41 +210,20 @@ __device__ void combine_segment(const AttnArgs& a, int h, int first, int n_slots
   }
 }
 
-// A piece of work as the kernel sees it (one plan record).
-struct Piece {
-  int h, b_begin, b_end, slot, row_start, q_len, ctx, comb, comb_first, comb_slots;
-  int64_t seq_id;
-};
-
-__device__ inline Piece read_piece(const int32_t* r) {
-  Piece p;
-  p.h = r[kPieceHead];
-  p.b_begin = r[kPieceBlkBegin];
-  p.b_end = r[kPieceBlkEnd];
-  p.slot = r[kPieceSlot];
-  p.row_start = r[kPieceRowStart];
-  p.q_len = r[kPieceQLen];
-  p.seq_id = r[kPieceSeqId];
-  p.ctx = r[kPieceCtx];
-  p.comb = r[kPieceComb];
-  p.comb_first = r[kPieceCombFirst];
-  p.comb_slots = r[kPieceCombSlots];
-  return p;
-}
-
-__device__ inline Piece read_piece_lds(const int32_t* __restrict__ rec_base, int i) {
-  return read_piece(rec_base + kPieceWords * i);
-}
-
 template <int NT>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(Tune<NT>::waves)))
+__global__ __launch_bounds__(Tune<NT>::waves * kWave)
+__attribute__((amdgpu_waves_per_eu(Tune<NT>::waves / 4)))
 void paged_attn_kernel(AttnArgs a) {
-  constexpr int NSTAGE = Tune<NT>::stages;
-  constexpr int MINB = 2 * NSTAGE;  // blocks per wave and piece, after padding, at least
-  constexpr int kPad = INT32_MIN;   // block id of a padding block (masked, reads block 0)
+  constexpr int NW = Tune<NT>::waves;
+  constexpr int S = Tune<NT>::stages;       // ring depth = blocks per claimed group
+  constexpr int NTHR = NW * kWave;
+  constexpr int QU = NT * 16 * (D / 8);     // 16-byte units of the staged Q rows
+  constexpr int QI = (QU + NTHR - 1) / NTHR;
+  constexpr int kPad = INT32_MIN;           // block id of a padding block (masked, reads block 0)
   extern __shared__ __align__(16) char smem_raw[];
-  __shared__ int s_last[kMaxWorkerPieces];  // piece pc completed its split segment: combine it
   __shared__ int32_t s_rec[kMaxWorkerPieces * kPieceWords];  // this worker's piece records
+  __shared__ int s_last[kMaxWorkerPieces];  // piece pc completed its split segment: combine it
+  __shared__ int s_claim;                   // first group of blocks nobody has claimed
   lds_char* smem = (lds_char*)smem_raw;
   lds_char* s_q = smem;                                   // [NT*16][ROWB]
   float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [NW][NT*16][RS] (aliases V)
@@ -257,64 +238,89 @@ void paged_attn_kernel(AttnArgs a) {
   // token 4g + a/4, dims 4*(a%4) .. +3
   const lds_char* tr_src = s_v + (4 * lg + (lr >> 2)) * ROWB + 8 * (lr & 3);
 
-  const int32_t* wrow = a.workers + kWorkerWords * worker_id();
-  const int p_begin = wrow[0], p_end = wrow[1];
-  if (p_begin >= p_end) return;  // whole workgroup idle
-  const int n_pc = p_end - p_begin;  // <= kMaxWorkerPieces (checked on the host)
-  for (int i = threadIdx.x; i < n_pc * kPieceWords; i += NW * kWave)
-    s_rec[i] = a.pieces[(int64_t)p_begin * kPieceWords + i];
+  // The worker's records sit at a fixed stride in the plan, so they load in
+  // parallel with the worker-table row that counts them.
+  const int wid = worker_id();
+  const int32_t* wrow = a.workers + kWorkerWords * wid;
+  const int n_pc = wrow[1] - wrow[0];  // <= piece_stride <= kMaxWorkerPieces (host-checked)
+  const int32_t* recs = a.pieces + (int64_t)wid * a.piece_stride * kPieceWords;
+  for (int i = threadIdx.x; i < a.piece_stride * kPieceWords; i += NTHR) s_rec[i] = recs[i];
   if (threadIdx.x < kMaxWorkerPieces) s_last[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_claim = NW;  // groups 0 .. NW-1 go one per wave
+  __syncthreads();
 
-  // Arrival protocol of split segments.  Each arrival is released by the
-  // wave that made the stores: a segment counts comb_slots * NW arrivals and
-  // whoever brings the last one merges the segment's partials at the end of
-  // its work.  A piece that is not the workgroup's last counts its waves'
-  // arrivals without stalling: each wave adds its arrival once it has
-  // consumed a block whose loads it issued after its partial stores (vector
-  // memory operations of a wave complete in order).
-  int pend_comb = -1, pend_pc = -1, pend_target = 0;  // arrival not yet counted
-  int done_comb = -1, done_pc = -1, done_target = 0, done_old = 0;  // counted, not yet checked
-
-  // This wave's blocks of a piece are b_begin + wave + NW*k, k < wave_blocks;
-  // the wave runs at least MINB and a multiple of NSTAGE blocks per piece,
-  // the extra ones being padding.
-  auto wave_blocks = [&](const Piece& p) {
-    const int n = p.b_end - p.b_begin;
-    return n > wave ? (n - wave + NW - 1) / NW : 0;
+  // Group g of the worker is blocks [S*j, S*j + S) of the piece p holding it,
+  // j = g - (groups of the pieces before p); each wave processes the groups
+  // it claims in claim order, so its groups only grow.
+  auto rec = [&](int p, int f) {
+    return __builtin_amdgcn_readfirstlane(s_rec[p * kPieceWords + f]);
   };
-  auto padded = [&](int nk) { return nk <= MINB ? MINB : (nk + NSTAGE - 1) / NSTAGE * NSTAGE; };
-  // Raw block ids of this wave's blocks k0 .. k0+63 of piece p, one per lane.
-  auto load_ids = [&](const Piece& p, int pnk, int k0) -> int {
-    const int kk = k0 + lane;
-    return kk < pnk ? a.bt[p.seq_id * a.bt_stride + p.b_begin + wave + NW * kk] : kPad;
+  auto gstart = [&](int p) { return p == 0 ? 0 : rec(p - 1, kPieceGroupEnd); };
+  const int n_groups = n_pc > 0 ? rec(n_pc - 1, kPieceGroupEnd) : 0;
+  // piece of group g, searching on from piece p; n_pc past the last group
+  auto resolve = [&](int g, int p) {
+    if (g >= n_groups) return n_pc;
+    while (g >= rec(p, kPieceGroupEnd)) ++p;
+    return p;
   };
-  // Q rows of piece p (zero padded), 16 B per thread and step.
-  auto load_q = [&](const Piece& p, u32x4 (&qv)[NT]) {
-    const int n_rows = p.q_len * a.gqa;
+  // raw block ids of group g of piece p in lanes 0 .. S-1 (kPad past the piece)
+  auto group_ids = [&](int g, int p) -> int {
+    int64_t idx = 0;
+    bool ok = false;
+    if (p < n_pc) {
+      const int b0 = rec(p, kPieceBlkBegin);
+      const int blk = (g - gstart(p)) * S + lane;
+      ok = lane < S && blk < rec(p, kPieceBlkEnd) - b0;
+      idx = (int64_t)rec(p, kPieceSeqId) * a.bt_stride + b0 + blk;
+    }
+    const int v = a.bt[ok ? idx : 0];
+    return ok ? v : kPad;
+  };
+  auto claim_group = [&]() {  // lane 0 receives the claimed group
+    int c = 0;
+    if (lane == 0) c = atomicAdd(&s_claim, 1);
+    return c;
+  };
+  auto head_base = [&](const f16* cache, int p) {
+    const int h = p < n_pc ? rec(p, kPieceHead) : 0;
+    return cache + ((int64_t)a.layer * a.hkv + h) * BS * D;
+  };
+  // Q rows of piece p, 16 B per thread and step (unit u: row u/16, column
+  // u%16).  Every lane loads: lanes past the piece's rows (or past the last
+  // piece) read q[0], and staging writes zeros for them.
+  auto q_rows = [&](int p) { return p < n_pc ? rec(p, kPieceQLen) * a.gqa : 0; };
+  auto store_q = [&](int p, const u32x4 (&qv)[QI]) {
+    const int n_rows = q_rows(p);
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const int u = threadIdx.x + i * NW * kWave;  // 16-byte unit: row u/16, column u%16
-      const int n = u >> 4;
-      qv[i] = u32x4{0u, 0u, 0u, 0u};
-      if (n < n_rows) {
-        const int qi = n / a.gqa, gh = n - qi * a.gqa;
-        qv[i] = *reinterpret_cast<const u32x4*>(
-            a.q + ((int64_t)(p.row_start + qi) * a.hq + p.h * a.gqa + gh) * D + (u & 15) * 8);
-      }
+    for (int i = 0; i < QI; ++i) {
+      const int u = threadIdx.x + i * NTHR;
+      if (u < QU)
+        *(lds_u32x4*)(s_q + (u >> 4) * ROWB + (u & 15) * 16) =
+            (u >> 4) < n_rows ? qv[i] : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto head_base = [&](const f16* cache, const Piece& p) {
-    return cache + ((int64_t)a.layer * a.hkv + p.h) * BS * D;
+  auto load_q = [&](int p, u32x4 (&qv)[QI]) {
+    const int n_rows = q_rows(p);
+    const int row_start = p < n_pc ? rec(p, kPieceRowStart) : 0;
+    const int h = p < n_pc ? rec(p, kPieceHead) : 0;
+#pragma unroll
+    for (int i = 0; i < QI; ++i) {
+      const int n = (threadIdx.x + i * NTHR) >> 4;
+      const int qi = n / a.gqa, gh = n - qi * a.gqa;
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          a.q + ((int64_t)(row_start + qi) * a.hq + h * a.gqa + gh) * D + (threadIdx.x & 15) * 8);
+      qv[i] = *(n < n_rows ? src : reinterpret_cast<const u32x4*>(a.q));
+    }
   };
 
-  // Ring of in-flight K/V blocks; block k of a piece lives in stage k % NSTAGE.
-  // Every refill issues its loads (a padding or out-of-pool block reads pool
-  // block 0 and is masked), so the compiler counts the loads in flight
-  // behind each block exactly and never drains the ring early.
+  // Ring of in-flight K/V blocks: stage st holds block st of a group.  Every
+  // refill issues its loads (a padding or out-of-pool block reads pool block
+  // 0 and is masked), so the compiler counts the loads in flight behind each
+  // block exactly and never drains the ring early.
   bool bad_block = false;  // reported once, at the end
-  f16x8 kr[NSTAGE][4];
-  u32x4 vr[NSTAGE][4];
-  int bid[NSTAGE];
+  f16x8 kr[S][4];
+  u32x4 vr[S][4];
+  int bid[S];
   // pool offset of block `id` (padding and bad ids read block 0; bid < 0 masks them)
   auto block_offset = [&](auto stage, int id) -> int64_t {
     constexpr int st = decltype(stage)::value;
@@ -335,57 +341,46 @@ void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) vr[st][i] = *reinterpret_cast<const u32x4*>(vp + 4 * i * D);
   };
-  // id of this wave's block k (< 128) from the two 64-id vectors of a piece
-  auto pick_id = [&](int lo, int hi, int k) {
-    return __builtin_amdgcn_readlane(k < 64 ? lo : hi, k & 63);
-  };
 
-  Piece cur = read_piece(wrow + kWorkerFirstPiece);
-  int nk = wave_blocks(cur);
-  int nkp = padded(nk);
-  int ids_lo = load_ids(cur, nk, 0);
-  int ids_hi = load_ids(cur, nk, 64);
-  u32x4 qv[NT];
-  load_q(cur, qv);
-  const f16* kbase = head_base(a.k_cache, cur);
-  const f16* vbase = head_base(a.v_cache, cur);
-  static_for<NSTAGE>([&](auto st) {
-    constexpr int s = decltype(st)::value;
-    const int64_t off = block_offset(st, s < nk ? pick_id(ids_lo, ids_hi, s) : kPad);
-    issue_k(st, kbase, off);
-    issue_v(st, vbase, off);
-  });
+  // Claims run one group ahead of the refills: while group g_cur is
+  // processed, the ring is refilled with g_nxt (ids known) and the ids of
+  // the group after it are loaded.
+  // Q of the first piece loads first, so staging it waits for nothing else.
+  u32x4 qv[QI];
+  load_q(0, qv);
+  int g_cur = wave;
+  const int p_cur = resolve(g_cur, 0);
+  const int cur_ids = group_ids(g_cur, p_cur);
+  int g_nxt = __builtin_amdgcn_readfirstlane(claim_group());
+  int p_nxt = resolve(g_nxt, p_cur);
+  int nxt_ids = group_ids(g_nxt, p_nxt);
+  int claim = claim_group();  // the group after g_nxt
+  {
+    const f16* kb = head_base(a.k_cache, p_cur);
+    const f16* vb = head_base(a.v_cache, p_cur);
+    static_for<S>([&](auto st) {
+      const int64_t off = block_offset(st, __builtin_amdgcn_readlane(cur_ids, decltype(st)::value));
+      issue_k(st, kb, off);
+      issue_v(st, vb, off);
+    });
+  }
+  const f16* kb_n = head_base(a.k_cache, p_nxt);
+  const f16* vb_n = head_base(a.v_cache, p_nxt);
+  store_q(0, qv);
 
   for (int pc = 0; pc < n_pc; ++pc) {
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const int u = threadIdx.x + i * NW * kWave;
-      *(lds_u32x4*)(s_q + (u >> 4) * ROWB + (u & 15) * 16) = qv[i];
-    }
-    __syncthreads();  // Q staged (and, the first time, the piece records)
+    __syncthreads();  // Q staged; every wave is past the previous piece's merge
 
-    // Next piece: record, ids and Q now, its first blocks in this piece's
-    // last group (so the ring runs on across the piece boundary).
-    const bool has_next = pc + 1 < n_pc;
-    Piece nxt = cur;
-    int nxt_nk = 0, nxt_lo = kPad, nxt_hi = kPad;
-    if (has_next) {
-      nxt = read_piece_lds(s_rec, pc + 1);
-      nxt_nk = wave_blocks(nxt);
-      nxt_lo = load_ids(nxt, nxt_nk, 0);
-      nxt_hi = load_ids(nxt, nxt_nk, 64);
-      load_q(nxt, qv);
-    }
-    const f16* nxt_kbase = head_base(a.k_cache, nxt);
-    const f16* nxt_vbase = head_base(a.v_cache, nxt);
-
-    const int n_rows = cur.q_len * a.gqa;
-    const int total = cur.ctx + cur.q_len;  // tokens of the segment
+    const int q_len = rec(pc, kPieceQLen), ctx = rec(pc, kPieceCtx);
+    const int b_begin = rec(pc, kPieceBlkBegin);
+    const int g_begin = gstart(pc), g_end = rec(pc, kPieceGroupEnd);
+    const int n_rows = q_len * a.gqa;
+    const int total = ctx + q_len;  // tokens of the segment
     int sl[NT];  // seq_len of the lane's row (causal bound inside the group)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int n = 16 * j + lr;
-      sl[j] = n < n_rows ? cur.ctx + n / a.gqa + 1 : total;
+      sl[j] = n < n_rows ? ctx + n / a.gqa + 1 : total;
     }
     float m[NT], l[NT];
     f32x4 acc[NT][8];
@@ -396,13 +391,12 @@ void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    int g_nn = 0, p_nn = n_pc, nn_ids = kPad;  // the group after g_nxt
 
-    // One block: scores, refill the stage, stage V, softmax, PV.  `last`
-    // (compile time): the refill block is in the next piece.
-    auto step = [&](auto stage, auto last, int k) {
+    // One block: scores, refill the stage, stage V, softmax, PV.  `blk` is
+    // the block's index in the segment.
+    auto step = [&](auto stage, int blk) {
       constexpr int st = decltype(stage)::value;
-      constexpr bool kLast = decltype(last)::value;
-      const int blk = cur.b_begin + wave + NW * k;
       // S^T: lane (lg, lr) gets scores of row 16j+lr for tokens 16*blk + 4lg + i.
       // (Q is re-read from LDS every block rather than held in registers.)
       const lds_char* qrow = s_q + lr * ROWB + lg * 16;
@@ -419,32 +413,15 @@ void paged_attn_kernel(AttnArgs a) {
         s[j] = t;
       }
       if constexpr (st == 0) {
-        if (pend_comb >= 0 && k == NSTAGE) {
-          // block NSTAGE of this piece was loaded after the previous piece's
-          // partial stores: once its K is here, so are they
-          asm volatile("" ::"v"(kr[0][0]) : "memory");
-          done_old = 0;
-          if (lane == 0)
-            done_old = __hip_atomic_fetch_add(a.counters + pend_comb, 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-          done_comb = pend_comb;
-          done_pc = pend_pc;
-          done_target = pend_target;
-          pend_comb = -1;
-        }
+        // the group after g_nxt: its ids load ahead of this group's refills
+        g_nn = __builtin_amdgcn_readfirstlane(claim);
+        p_nn = resolve(g_nn, p_nxt);
+        nn_ids = group_ids(g_nn, p_nn);
+        claim = claim_group();
       }
-      // refill this stage with block k + NSTAGE of this piece or the next:
-      // K now, V once this block's V is staged in LDS (tokens 4i + lg)
-      const int kn = k + NSTAGE;
-      const f16* kb_n = kLast ? nxt_kbase : kbase;
-      const f16* vb_n = kLast ? nxt_vbase : vbase;
-      int id_n;
-      if constexpr (!kLast) {
-        id_n = kn < nk ? pick_id(ids_lo, ids_hi, kn) : kPad;
-      } else {
-        const int jn = kn - nkp;
-        id_n = has_next && jn < nxt_nk ? __builtin_amdgcn_readlane(nxt_lo, jn) : kPad;
-      }
+      // refill this stage with block st of g_nxt: K now, V once this
+      // block's V is staged in LDS (tokens 4i + lg)
+      const int id_n = __builtin_amdgcn_readlane(nxt_ids, st);
       const bool valid = bid[st] >= 0;
       const int64_t off_n = block_offset(stage, id_n);
       issue_k(stage, kb_n, off_n);
@@ -490,14 +467,32 @@ void paged_attn_kernel(AttnArgs a) {
       }
     };
 
-    // Groups whose refills stay in this piece (at least one: nkp >= 2*NSTAGE),
-    // then the last group, whose refills start the next piece.
-    int k = 0;
-    do {
-      static_for<NSTAGE>([&](auto st) { step(st, std::false_type{}, k + decltype(st)::value); });
-      k += NSTAGE;
-    } while (k + NSTAGE < nkp);
-    static_for<NSTAGE>([&](auto st) { step(st, std::true_type{}, k + decltype(st)::value); });
+    // This wave's groups of the piece; the ring carries on into the next
+    // piece's groups (or padding) without draining.
+    auto group = [&]() {
+      // The next piece's Q is loaded ahead of the refills of this wave's last
+      // group of the piece (g_nxt lies past it), so the merge that stages it
+      // waits for it with the count of loads behind it known.
+      if (g_nxt >= g_end && pc + 1 < n_pc) load_q(pc + 1, qv);
+      const int blk0 = b_begin + (g_cur - g_begin) * S;
+      static_for<S>([&](auto st) { step(st, blk0 + decltype(st)::value); });
+      g_cur = g_nxt;
+      g_nxt = g_nn;
+      p_nxt = p_nn;
+      nxt_ids = nn_ids;
+      kb_n = head_base(a.k_cache, p_nxt);
+      vb_n = head_base(a.v_cache, p_nxt);
+    };
+    if (g_cur < g_end) {
+      do group();
+      while (g_cur < g_end);
+    } else if (pc + 1 < n_pc) {
+      // no group of this piece: load the next Q and wait for it now (this
+      // wave has nothing to overlap until the merge)
+      load_q(pc + 1, qv);
+#pragma unroll
+      for (int i = 0; i < QI; ++i) asm volatile("" : "+v"(qv[i]));
+    }
 
     // Row sums across the four k-groups.
 #pragma unroll
@@ -506,10 +501,12 @@ void paged_attn_kernel(AttnArgs a) {
       l[j] += __shfl_xor(l[j], 32, kWave);
     }
 
-    // Merge the four waves' states in one round: every wave writes its
-    // live rows (acc, m, l) to LDS, then all threads combine them, four dims
-    // per thread and step, and write the fp16 output (or the fp32 partial).
-    __syncthreads();  // every wave is done with its V staging (aliased below)
+    // Merge the waves' states in one round: every wave writes its live rows
+    // (acc, m, l; empty if it took no group of the piece) to LDS, then all
+    // threads combine them, four dims per thread and step, and write the
+    // fp16 output (or the fp32 partial).
+    __syncthreads();  // every wave is done with its V staging (aliased below) and Q
+    if (pc + 1 < n_pc) store_q(pc + 1, qv);
     {
       float* ma = s_acc + wave * NT * 16 * RS;
       float* mm = s_ml + wave * 2 * NT * 16;
@@ -529,10 +526,12 @@ void paged_attn_kernel(AttnArgs a) {
     }
     __syncthreads();
     {
+      const int slot = rec(pc, kPieceSlot), row_start = rec(pc, kPieceRowStart);
+      const int h = rec(pc, kPieceHead);
       const __amdgpu_buffer_rsrc_t rpart =
-          raw_buffer(a.part_o + (int64_t)(cur.slot < 0 ? 0 : cur.slot) * a.rows_max * D,
+          raw_buffer(a.part_o + (int64_t)(slot < 0 ? 0 : slot) * a.rows_max * D,
                      (uint32_t)a.rows_max * D * 4);
-      for (int idx = threadIdx.x; idx < n_rows * (D / 4); idx += NW * kWave) {
+      for (int idx = threadIdx.x; idx < n_rows * (D / 4); idx += NTHR) {
         const int n = idx / (D / 4), c4 = idx % (D / 4);
         float mw[NW], lw[NW], M = -INFINITY;
 #pragma unroll
@@ -545,7 +544,7 @@ void paged_attn_kernel(AttnArgs a) {
         f32x4 ov = {0.f, 0.f, 0.f, 0.f};
         float L = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
+        for (int w = 0; w < NW; ++w) {  // a wave with no block of the piece has m = -inf
           const float f = exp2f(mw[w] - M_use);
           L += lw[w] * f;
           ov += *reinterpret_cast<const f32x4*>(s_acc + (w * NT * 16 + n) * RS + 4 * c4) * f;
@@ -553,64 +552,44 @@ void paged_attn_kernel(AttnArgs a) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
         ov *= inv;
         const int qi = n / a.gqa, gh = n - qi * a.gqa;
-        const int64_t orow = (int64_t)(cur.row_start + qi) * a.hq + cur.h * a.gqa + gh;
+        const int64_t orow = (int64_t)(row_start + qi) * a.hq + h * a.gqa + gh;
         const float lse2 = L > 0.f ? M + __log2f(L) : -INFINITY;
-        if (cur.slot < 0) {
+        if (slot < 0) {
           f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
           *reinterpret_cast<f16x4*>(a.o + orow * D + 4 * c4) = hv;
           if (c4 == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
         } else {
           store_coherent(rpart, ((uint32_t)n * D + 4 * c4) * 4, ov);
           if (c4 == 0)
-            __hip_atomic_store(a.part_lse + (int64_t)cur.slot * a.rows_max + n, lse2,
+            __hip_atomic_store(a.part_lse + (int64_t)slot * a.rows_max + n, lse2,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
-    // Arrivals of split segments (see above).  The previous piece's arrival
-    // was counted during this piece: note whether it was the last one.
-    if (done_comb >= 0) {
-      if (lane == 0 && done_old == done_target - 1) s_last[done_pc] = 1;
-      done_comb = -1;
-    }
-    if (cur.slot >= 0) {
-      const int target = cur.comb_slots * NW;
-      if (has_next) {
-        pend_comb = cur.comb;
-        pend_pc = pc;
-        pend_target = target;
-      } else {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keeps the stores above
-        __builtin_amdgcn_s_waitcnt(0);                           // ... and completed
-        __syncthreads();
-        if (threadIdx.x == 0) {
-          const int old = __hip_atomic_fetch_add(a.counters + cur.comb, NW, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-          if (old == target - NW) s_last[pc] = 1;
-        }
-      }
-    }
-    // The next piece restages Q (s_q is not aliased by the merge area, and
-    // every read of it ended before the merge barriers); its first blocks
-    // are already in the ring.
-    if (has_next) {
-      cur = nxt;
-      nk = nxt_nk;
-      nkp = padded(nk);
-      ids_lo = nxt_lo;
-      ids_hi = nxt_hi;
-      kbase = nxt_kbase;
-      vbase = nxt_vbase;
+  }
+
+  // Arrivals of split segments, once every wave's partial stores are
+  // complete: one per piece, and the workgroup that brings a segment's last
+  // arrival merges its partials.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // keeps the stores above
+  __builtin_amdgcn_s_waitcnt(0);                           // ... and completed
+  __syncthreads();
+  if (threadIdx.x < n_pc) {
+    const int32_t* r = s_rec + threadIdx.x * kPieceWords;
+    if (r[kPieceSlot] >= 0) {
+      const int old = __hip_atomic_fetch_add(a.counters + r[kPieceComb], 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      if (old == r[kPieceCombSlots] - 1) s_last[threadIdx.x] = 1;
     }
   }
-  // Merge the segments whose last arrival this workgroup brought.
   __syncthreads();
   for (int pc = 0; pc < n_pc; ++pc) {
     if (s_last[pc]) {
-      const Piece p = read_piece_lds(s_rec, pc);
-      combine_segment(a, p.h, p.comb_first, p.comb_slots, p.row_start, p.q_len * a.gqa);
+      combine_segment(a, rec(pc, kPieceHead), rec(pc, kPieceCombFirst), rec(pc, kPieceCombSlots),
+                      rec(pc, kPieceRowStart), rec(pc, kPieceQLen) * a.gqa);
       if (threadIdx.x == 0)
-        __hip_atomic_store(a.counters + p.comb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.counters + rec(pc, kPieceComb), 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (bad_block) flag_status(a.status, NSD_STATUS_BAD_BLOCK);
@@ -627,7 +606,8 @@ int launch_nt(const AttnArgs& args, int grid, hipStream_t stream) {
       return fail(NSD_ERR_HIP, "paged_attention: LDS attribute: %s", hipGetErrorString(e));
     attr_set = true;
   }
-  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(NW * kWave), lds_bytes<NT>(), stream,
+  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(Tune<NT>::waves * kWave),
+                     lds_bytes<NT>(), stream,
                      args);
   return launch_status("paged_attention");
 }
@@ -635,7 +615,7 @@ int launch_nt(const AttnArgs& args, int grid, hipStream_t stream) {
 template <int NT>
 int occupancy_nt(int* blocks) {
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-             blocks, reinterpret_cast<const void*>(&paged_attn_kernel<NT>), NW * kWave,
+             blocks, reinterpret_cast<const void*>(&paged_attn_kernel<NT>), Tune<NT>::waves * kWave,
              lds_bytes<NT>()) == hipSuccess
              ? NSD_OK
              : NSD_ERR_HIP;
@@ -686,29 +666,47 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   const int grid = plan_host[kPlanWorkers];
   const int n_combine = plan_host[kPlanCombines];
   const int rows_max = plan_host[kPlanRowsMax];
-  if (plan_host[kPlanRows] == 0 || grid == 0) return NSD_OK;
+  const int n_rows_plan = plan_host[kPlanRows];
+  if (n_rows_plan == 0 || grid == 0) return NSD_OK;
   if (!q || !o || !k_cache || !v_cache || !block_table)
     return fail(NSD_ERR_INVALID, "paged_attention: null pointer");
   if (!aligned16(q) || !aligned16(o) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(NSD_ERR_INVALID, "paged_attention: q/o/caches must be 16-byte aligned");
-  if (rows_max < 1 || rows_max > kMaxGroupRows || grid % 8 != 0)
+  const int nt = (rows_max + 15) / 16;
+  const int stride = plan_host[kPlanPieceStride];
+  const int64_t n_slots = plan_host[kPlanSlots];
+  if (rows_max < 1 || rows_max > kMaxGroupRows || grid % 8 != 0 || stride < 1 ||
+      stride > kMaxWorkerPieces || (int64_t)plan_host[kPlanPieces] != (int64_t)grid * stride ||
+      plan_host[kPlanRingStages] != ring_stages(nt) || n_slots < 0 || n_combine < 0)
     return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan header");
-  // the kernel keeps a worker's piece records in LDS and two 64-id vectors
-  // per wave and piece: enforce the planner's limits on this plan
+  // the kernel trusts the records it claims blocks from: check every one
+  // against the buffers and LDS layouts it will touch
+  const int gqa = num_q_heads / num_kv_heads;
   const int32_t* wt = plan_host + plan_host[kPlanOffWorkers];
   const int32_t* pr = plan_host + plan_host[kPlanOffPieces];
   for (int w = 0; w < grid; ++w) {
     const int32_t* row = wt + kWorkerWords * w;
-    if (row[1] - row[0] > kMaxWorkerPieces || row[0] < 0 || row[1] > plan_host[kPlanPieces])
+    if (row[0] != w * stride || row[1] < row[0] || row[1] - row[0] > stride)
       return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (worker %d)", w);
+    int64_t groups = 0;
+    for (int i = row[0]; i < row[1]; ++i) {
+      const int32_t* r = pr + kPieceWords * i;
+      const int nb = r[kPieceBlkEnd] - r[kPieceBlkBegin];
+      groups += (nb + ring_stages(nt) - 1) / ring_stages(nt);
+      const bool split_ok =
+          r[kPieceSlot] < 0 ||
+          (r[kPieceComb] >= 0 && r[kPieceComb] < n_combine && r[kPieceCombFirst] >= 0 &&
+           r[kPieceCombSlots] >= 1 && r[kPieceCombFirst] + (int64_t)r[kPieceCombSlots] <= n_slots &&
+           r[kPieceSlot] >= r[kPieceCombFirst] &&
+           r[kPieceSlot] < r[kPieceCombFirst] + r[kPieceCombSlots]);
+      if (r[kPieceBlkBegin] < 0 || nb < 1 || r[kPieceBlkEnd] > bt_stride || r[kPieceSeqId] < 0 ||
+          r[kPieceHead] < 0 || r[kPieceHead] >= num_kv_heads || r[kPieceQLen] < 1 ||
+          (int64_t)r[kPieceQLen] * gqa > rows_max || r[kPieceRowStart] < 0 ||
+          (int64_t)r[kPieceRowStart] + r[kPieceQLen] > n_rows_plan || r[kPieceGroupEnd] != groups ||
+          !split_ok)
+        return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (piece %d)", i);
+    }
   }
-  for (int i = 0; i < plan_host[kPlanPieces]; ++i) {
-    const int32_t* r = pr + kPieceWords * i;
-    if (r[kPieceBlkEnd] - r[kPieceBlkBegin] > kMaxPieceBlocks || r[kPieceBlkBegin] < 0 ||
-        r[kPieceBlkEnd] <= r[kPieceBlkBegin])
-      return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (piece %d)", i);
-  }
-  const int64_t n_slots = plan_host[kPlanSlots];
   const int64_t part_bytes = (n_slots * rows_max * (int64_t)(D + 1) * 4 + 255) / 256 * 256;
   const int64_t need = n_combine > 0 ? part_bytes + n_combine * 4 : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
@@ -735,12 +733,12 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   args.layer = layer;
   args.hq = num_q_heads;
   args.hkv = num_kv_heads;
-  args.gqa = num_q_heads / num_kv_heads;
+  args.gqa = gqa;
   args.rows_max = rows_max;
+  args.piece_stride = stride;
   args.scale_log2 = softmax_scale * 1.4426950408889634f;
 
   hipStream_t st = as_stream(stream);
-  const int nt = (rows_max + 15) / 16;
   switch (nt) {
     case 1: return launch_nt<1>(args, grid, st);
     case 2: return launch_nt<2>(args, grid, st);

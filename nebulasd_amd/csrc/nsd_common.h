@@ -30,11 +30,16 @@ enum PlanHeader {
   kPlanOffPieces,      // word offset of pieces [n_pieces][kPieceWords]
   kPlanOffCombines,    // word offset of combines [n_combines][kPieceWords]
   kPlanWords,          // total words
+  kPlanPieceStride,    // piece records per worker: worker w's records start at w * stride
+  kPlanRingStages,     // blocks per claimed group the records' group counts assume
 };
-static_assert(kPlanWords + 1 == NSD_PLAN_HEADER_WORDS, "plan header size");
+static_assert(kPlanRingStages < NSD_PLAN_HEADER_WORDS, "plan header size");
 
 // A piece: blocks [blk_begin, blk_end) of one (group, kv head) segment, with
 // the group's description inlined so a worker needs one record per piece.
+// The workgroup's waves claim a piece's blocks in groups of ring_stages(nt)
+// consecutive blocks; kPieceGroupEnd counts the groups of the worker's pieces
+// up to and including this one.
 enum PieceField {
   kPieceHead = 0,   // kv head
   kPieceBlkBegin,   // first 16-token block
@@ -47,23 +52,29 @@ enum PieceField {
   kPieceComb,       // combine record of the segment, or -1
   kPieceCombFirst,  // first partial slot of the segment
   kPieceCombSlots,  // partial slots of the segment
-  kPiecePad,
+  kPieceGroupEnd,   // groups of this worker's pieces 0 .. this one
   kPieceWords,
 };
-// A worker-table row: {first piece, end piece, <first piece record>, 0, 0},
-// so a workgroup reaches its first piece with a single 64-byte load.
+// A worker-table row: {first piece, end piece, <first piece record>, 0, 0}.
+// Worker w's records are pieces [w * stride, w * stride + count), so the
+// kernel loads them without reading the table first.
 constexpr int kWorkerWords = 16;
 constexpr int kWorkerFirstPiece = 2;
 // A combine record: {kv head, first slot, slot count, row start, q_len, 0, 0, 0}.
 enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
 
 constexpr int32_t kPlanMagicValue = 0x4E534450;
-constexpr int32_t kPlanVersionValue = 5;
+constexpr int32_t kPlanVersionValue = 6;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
 constexpr int kMaxGroupRows = 64;
 constexpr int kMaxSlotsPerSegment = 128;
 constexpr int kMaxWorkerPieces = 32;   // pieces one workgroup keeps records of
-constexpr int kMaxPieceBlocks = 512;   // 128 blocks per wave: two 64-id vectors
+
+// Attention kernel shape for groups of up to 16*nt query rows (nt = 1..4):
+// K/V ring depth, which is also the size of a claimed group of blocks, and
+// waves per workgroup (one workgroup per compute unit).
+constexpr int ring_stages(int nt) { return nt == 3 ? 2 : 1; }
+constexpr int attn_waves(int nt) { return nt <= 2 ? 8 : 4; }
 
 }  // namespace nsd

@@ -14,10 +14,10 @@ namespace nsd {
 namespace {
 thread_local std::string g_last_error;
 // Cost model of the planner, in 16-token blocks of streaming: a piece costs
-// its blocks (at least kMinPieceBlocks: a wave pads its share of a piece to
-// two ring lengths with masked blocks) plus a fixed kPieceCostBlocks for the
-// wave merge and output write at its end.
-constexpr int64_t kMinPieceBlocks = 24;
+// its blocks rounded up to whole claimed groups plus a fixed kPieceCostBlocks
+// for the wave merge and output write at its end.  A worker opens another
+// piece only if at least kMinPieceBlocks of its budget remain for it.
+constexpr int64_t kMinPieceBlocks = 4;
 constexpr int64_t kPieceCostBlocks = 8;
 }  // namespace
 
@@ -45,7 +45,9 @@ extern "C" int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_w
   if (n_rows < 0 || num_kv_heads <= 0 || n_workers <= 0) return -1;
   const int64_t segs = n_rows * num_kv_heads;
   const int64_t nw = round_up8(n_workers);
-  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kWorkerWords * nw + kPieceWords * (nw + segs) +
+  // piece records: at most min(32, pieces) per worker, at a fixed stride
+  const int64_t stride = std::min<int64_t>(kMaxWorkerPieces, nw + segs);
+  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kWorkerWords * nw + kPieceWords * nw * stride +
          kPieceWords * segs;
 }
 
@@ -110,8 +112,10 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   // 3. contiguous block ranges per worker of near-equal cost (the cost model
   //    above).  The target cost is the smallest one that fits the stream into
   //    the workers; it also keeps every segment under kMaxSlotsPerSegment
-  //    pieces, every piece under kMaxPieceBlocks blocks and every worker
-  //    under kMaxWorkerPieces pieces.
+  //    pieces and every worker under kMaxWorkerPieces pieces.
+  const int nt = std::max(1, (rows_max + 15) / 16);
+  const int64_t stages = ring_stages(nt);
+  auto groups_of = [&](int64_t blocks) { return (blocks + stages - 1) / stages; };
   int64_t max_seg = 0;
   for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
   const int64_t cmin = kPieceCostBlocks + std::max<int64_t>(
@@ -126,13 +130,12 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
       if (cuts) cuts->push_back(-1);  // worker marker
       while (pos < total && opened < kMaxWorkerPieces) {
         while (seg_start[seg_i + 1] <= pos) ++seg_i;
-        if (opened > 0 && budget <= kPieceCostBlocks + kMinPieceBlocks / 2) break;
+        if (opened > 0 && budget < kPieceCostBlocks + kMinPieceBlocks) break;
         const int64_t take = std::max<int64_t>(
-            1, std::min({budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos,
-                         (int64_t)kMaxPieceBlocks}));
+            1, std::min(budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos));
         if (cuts) cuts->insert(cuts->end(), {pos, pos + take});
         pos += take;
-        budget -= kPieceCostBlocks + std::max(take, kMinPieceBlocks);
+        budget -= kPieceCostBlocks + groups_of(take) * stages;
         ++opened;
         if (budget <= 0) break;
       }
@@ -141,7 +144,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
     return used;
   };
   const int64_t want = std::max<int64_t>(1, n_workers);
-  int64_t lo = cmin, hi = std::max(cmin, total + kPieceCostBlocks);
+  int64_t lo = cmin, hi = std::max(cmin, total + n_segs * (kPieceCostBlocks + stages));
   if (total > 0 && cut_stream(lo, nullptr) > want) {
     while (lo + 1 < hi) {  // smallest cap that fits in `want` workers
       const int64_t mid = (lo + hi) / 2;
@@ -153,7 +156,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t active = total > 0 ? cut_stream(lo, &cuts) : 0;
   const int64_t grid = total > 0 ? round_up8(active) : 0;
   std::vector<int32_t> wstart(grid + 1, 0);
-  std::vector<int32_t> pieces;  // kPieceWords per piece
+  std::vector<int32_t> pieces;  // kPieceWords per piece, workers' pieces in order
   int64_t seg = 0, w = -1;
   for (size_t c = 0; c < cuts.size();) {
     if (cuts[c] < 0) {  // next worker
@@ -205,21 +208,34 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   }
   const int64_t n_combines = (int64_t)combines.size() / kPieceWords;
 
-  // 5. worker table: piece range plus an inline copy of the first piece.
+  // 5. records at a fixed stride per worker (zero records fill the gaps),
+  //    each with its worker's running group count; the worker table holds
+  //    each worker's record range and an inline copy of its first record.
+  int64_t stride = 0;
+  for (int64_t v = 0; v < grid; ++v) stride = std::max<int64_t>(stride, wstart[v + 1] - wstart[v]);
+  std::vector<int32_t> records(kPieceWords * grid * stride, 0);
   std::vector<int32_t> wtable(kWorkerWords * grid, 0);
-  for (int64_t w = 0; w < grid; ++w) {
-    int32_t* row = &wtable[kWorkerWords * w];
-    row[0] = wstart[w];
-    row[1] = wstart[w + 1];
-    if (wstart[w] < wstart[w + 1])
-      std::copy(&pieces[kPieceWords * wstart[w]], &pieces[kPieceWords * (wstart[w] + 1)],
+  for (int64_t v = 0; v < grid; ++v) {
+    int64_t groups_run = 0;
+    for (int64_t i = wstart[v]; i < wstart[v + 1]; ++i) {
+      int32_t* r = &records[kPieceWords * (v * stride + (i - wstart[v]))];
+      std::copy(&pieces[kPieceWords * i], &pieces[kPieceWords * (i + 1)], r);
+      groups_run += groups_of(r[kPieceBlkEnd] - r[kPieceBlkBegin]);
+      r[kPieceGroupEnd] = (int32_t)groups_run;
+    }
+    int32_t* row = &wtable[kWorkerWords * v];
+    row[0] = (int32_t)(v * stride);
+    row[1] = (int32_t)(v * stride + wstart[v + 1] - wstart[v]);
+    if (wstart[v] < wstart[v + 1])
+      std::copy(&records[kPieceWords * v * stride], &records[kPieceWords * (v * stride + 1)],
                 row + kWorkerFirstPiece);
   }
+  const int64_t n_records = grid * stride;
 
   const int64_t off_groups = NSD_PLAN_HEADER_WORDS;
   const int64_t off_wstart = off_groups + 4 * n_groups;
   const int64_t off_pieces = off_wstart + kWorkerWords * grid;
-  const int64_t off_combines = off_pieces + kPieceWords * n_pieces;
+  const int64_t off_combines = off_pieces + kPieceWords * n_records;
   const int64_t words = off_combines + kPieceWords * n_combines;
   if (words > plan_capacity) {
     *plan_words = words;  // so the caller can retry with a large enough buffer
@@ -230,11 +246,12 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
     return fail(NSD_ERR_INVALID, "plan: too large (%lld words)", (long long)words);
 
   int32_t* h = plan;
+  std::fill(h, h + NSD_PLAN_HEADER_WORDS, 0);
   h[kPlanMagic] = kPlanMagicValue;
   h[kPlanVersion] = kPlanVersionValue;
   h[kPlanRows] = (int32_t)n_rows;
   h[kPlanGroups] = (int32_t)n_groups;
-  h[kPlanPieces] = (int32_t)n_pieces;
+  h[kPlanPieces] = (int32_t)n_records;
   h[kPlanWorkers] = (int32_t)grid;
   h[kPlanCombines] = (int32_t)n_combines;
   h[kPlanSlots] = (int32_t)n_slots;
@@ -246,9 +263,11 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   h[kPlanOffPieces] = (int32_t)off_pieces;
   h[kPlanOffCombines] = (int32_t)off_combines;
   h[kPlanWords] = (int32_t)words;
+  h[kPlanPieceStride] = (int32_t)stride;
+  h[kPlanRingStages] = (int32_t)stages;
   std::copy(groups.begin(), groups.end(), h + off_groups);
   std::copy(wtable.begin(), wtable.end(), h + off_wstart);
-  std::copy(pieces.begin(), pieces.end(), h + off_pieces);
+  std::copy(records.begin(), records.end(), h + off_pieces);
   std::copy(combines.begin(), combines.end(), h + off_combines);
 
   *plan_words = words;

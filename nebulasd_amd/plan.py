@@ -68,25 +68,36 @@ def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim:
 
 
 def decode_plan(words: np.ndarray) -> dict:
-    """Split plan words into named numpy views (for inspection and tests)."""
+    """Split plan words into named numpy views (for inspection and tests).
+
+    Worker w's piece records sit at ``records[w * piece_stride :]`` (the
+    kernel reads them without the worker table); ``pieces`` lists the used
+    records in worker order and ``worker_start`` indexes it.
+    """
     h = words[:_lib.PLAN_HEADER_WORDS]
-    n_groups, n_pieces = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_PIECES])
+    n_groups, n_records = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_PIECES])
     n_workers, n_comb = int(h[_lib.PLAN_WORKERS]), int(h[_lib.PLAN_COMBINES])
     og, ow = int(h[_lib.PLAN_OFF_GROUPS]), int(h[_lib.PLAN_OFF_WSTART])
     op, oc = int(h[_lib.PLAN_OFF_PIECES]), int(h[_lib.PLAN_OFF_COMBINES])
+    table = words[ow:ow + WORKER_WORDS * n_workers].reshape(n_workers, WORKER_WORDS)
+    # {kv head, blk_begin, blk_end, slot, row_start, q_len, seq_id, ctx,
+    #  combine, combine first slot, combine slots, worker's groups so far}
+    records = words[op:op + PIECE_WORDS * n_records].reshape(n_records, PIECE_WORDS)
+    used = [i for w in range(n_workers) for i in range(int(table[w, 0]), int(table[w, 1]))]
+    counts = [int(table[w, 1] - table[w, 0]) for w in range(n_workers)]
     return {
         "rows": int(h[_lib.PLAN_ROWS]),
         "workers": n_workers,
         "slots": int(h[_lib.PLAN_SLOTS]),
         "rows_max": int(h[_lib.PLAN_ROWS_MAX]),
+        "piece_stride": int(h[_lib.PLAN_PIECE_STRIDE]),
+        "ring_stages": int(h[_lib.PLAN_RING_STAGES]),
         "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
-        # per worker: {first piece, end piece, <first piece record>, 0...}
-        "workers_table": words[ow:ow + WORKER_WORDS * n_workers].reshape(n_workers, WORKER_WORDS),
-        "worker_start": np.append(words[ow:ow + WORKER_WORDS * n_workers:WORKER_WORDS],
-                                  words[ow + WORKER_WORDS * (n_workers - 1) + 1] if n_workers else 0),
-        # {kv head, blk_begin, blk_end, slot, row_start, q_len, seq_id, ctx,
-        #  combine, combine first slot, combine slots, 0}
-        "pieces": words[op:op + PIECE_WORDS * n_pieces].reshape(n_pieces, PIECE_WORDS),
+        # per worker: {first record, end record, <first record>, 0...}
+        "workers_table": table,
+        "records": records,
+        "pieces": records[used] if used else records[:0],
+        "worker_start": np.concatenate([[0], np.cumsum(counts)]).astype(np.int64),
         # {kv head, first_slot, n_slots, row_start, q_len, 0 ...}
         "combines": words[oc:oc + PIECE_WORDS * n_comb].reshape(n_comb, PIECE_WORDS),
     }

@@ -69,7 +69,13 @@ def test_error_paths_without_gpu(lib):
 
 
 # planner constants (nebulasd_amd/csrc/nsd_common.h, nsd_host.cpp)
-MAX_WORKER_PIECES, MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, PIECE_COST = 32, 512, 24, 8
+MAX_WORKER_PIECES, MIN_PIECE_BLOCKS, PIECE_COST = 32, 4, 8
+
+
+def ring_stages(rows_max):
+    """Blocks per claimed group for groups of up to rows_max query rows."""
+    nt = (rows_max + 15) // 16
+    return 2 if nt == 3 else 1
 
 
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
@@ -97,7 +103,7 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
     last = (-1, -1)
     for w in range(p["workers"]):
         for pc in range(ws[w], ws[w + 1]):
-            h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, pad = (
+            h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, gend = (
                 int(x) for x in pieces[pc])
             seg = seg_of[(row_start, h)]
             g = groups[seg // hkv]
@@ -129,24 +135,38 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
             assert (int(c[3]), int(c[0])) == (int(pcs[4]), int(pcs[0]))
             assert (cfirst, cslots) == (int(c[1]), int(c[2]))
             assert cfirst <= int(pcs[3]) < cfirst + cslots
-    # the worker table inlines each worker's first piece
+    # records sit at a fixed stride per worker (zero records in the gaps);
+    # the worker table holds each worker's record range and first record
+    stride, recs = p["piece_stride"], p["records"]
+    assert len(recs) == p["workers"] * stride
     for w in range(p["workers"]):
         row = p["workers_table"][w]
-        assert (row[0], row[1]) == (ws[w], ws[w + 1])
-        if ws[w] < ws[w + 1]:
+        n = ws[w + 1] - ws[w]
+        assert (row[0], row[1]) == (w * stride, w * stride + n) and n <= stride
+        assert (recs[w * stride:w * stride + n] == pieces[ws[w]:ws[w + 1]]).all()
+        assert (recs[w * stride + n:(w + 1) * stride] == 0).all()
+        if n:
             assert list(row[2:14]) == list(pieces[ws[w]])
-    # planner limits: pieces per worker, blocks per piece
+    # each record counts its worker's groups of ring-depth blocks so far
+    stages = ring_stages(p["rows_max"])
+    assert p["ring_stages"] == stages
+    for w in range(p["workers"]):
+        run = 0
+        for pc in range(ws[w], ws[w + 1]):
+            run += -(-int(pieces[pc][2] - pieces[pc][1]) // stages)
+            assert int(pieces[pc][11]) == run
+    # planner limits: pieces per worker
     for w in range(p["workers"]):
         assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES
-    assert all(0 < int(pc[2] - pc[1]) <= MAX_PIECE_BLOCKS for pc in pieces)
-    # near-equal cost per active worker: max(blocks, 24) + 8 per piece; only
-    # the last active worker, or one stopped by the piece limit, may fall short
-    cost = [sum(max(int(pieces[pc][2] - pieces[pc][1]), MIN_PIECE_BLOCKS) + PIECE_COST
+    # near-equal cost per active worker: blocks rounded up to whole groups,
+    # plus 8 per piece; only the last active worker, or one stopped by the
+    # piece limit, may fall short
+    cost = [sum(-(-int(pieces[pc][2] - pieces[pc][1]) // stages) * stages + PIECE_COST
                 for pc in range(ws[w], ws[w + 1])) for w in range(p["workers"])]
     active = [w for w in range(p["workers"]) if cost[w] > 0]
     top = max(cost[w] for w in active)
     for w in active[:-1]:
-        assert cost[w] >= top - 2 * (PIECE_COST + MIN_PIECE_BLOCKS) or \
+        assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS + stages) or \
             ws[w + 1] - ws[w] == MAX_WORKER_PIECES, (w, cost[w], top)
     assert p["workers"] % 8 == 0
 
@@ -270,7 +290,7 @@ def test_plan_respects_kernel_limits(lib):
     p, _ = _plan(list(range(n)), [1] * n, hq=16, hkv=8, workers=8, bt_rows=n, stride=16)
     check_plan_invariants(p, list(range(n)), [1] * n, 8, 2)
     assert p["workers"] > 8
-    # one long request on one worker: pieces of at most 512 blocks
+    # one long request on one worker: one piece per kv head
     p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
-    assert max(int(c[2]) for c in p["combines"]) <= 128
+    assert len(p["pieces"]) == 8 and len(p["combines"]) == 0
