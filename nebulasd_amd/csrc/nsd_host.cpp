@@ -15,10 +15,12 @@ namespace {
 thread_local std::string g_last_error;
 // Cost model of the planner, in 16-token blocks of streaming: a piece costs
 // its blocks rounded up to whole claimed groups plus a fixed kPieceCostBlocks
-// for the wave merge and output write at its end.  A worker opens another
-// piece only if at least kMinPieceBlocks of its budget remain for it.
+// for what ends it (the waves drain and merge, and a split segment's partial
+// is written and merged later); 24 was the fastest of 8..48 on the
+// verify and decode shapes.  A worker opens another piece only if at least
+// kMinPieceBlocks of its budget remain for it.
 constexpr int64_t kMinPieceBlocks = 4;
-constexpr int64_t kPieceCostBlocks = 8;
+constexpr int64_t kPieceCostBlocks = 24;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {

@@ -69,7 +69,7 @@ def test_error_paths_without_gpu(lib):
 
 
 # planner constants (nebulasd_amd/csrc/nsd_common.h, nsd_host.cpp)
-MAX_WORKER_PIECES, MIN_PIECE_BLOCKS, PIECE_COST = 32, 4, 8
+MAX_WORKER_PIECES, MIN_PIECE_BLOCKS, PIECE_COST = 32, 4, 24
 
 
 def ring_stages(rows_max):
@@ -159,7 +159,7 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
     for w in range(p["workers"]):
         assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES
     # near-equal cost per active worker: blocks rounded up to whole groups,
-    # plus 8 per piece; only the last active worker, or one stopped by the
+    # plus 24 per piece; only the last active worker, or one stopped by the
     # piece limit, may fall short
     cost = [sum(-(-int(pieces[pc][2] - pieces[pc][1]) // stages) * stages + PIECE_COST
                 for pc in range(ws[w], ws[w + 1])) for w in range(p["workers"])]
