@@ -16,14 +16,14 @@
 // block is already the P^T operand of the PV product (lane group g holds
 // tokens 4g..4g+3).
 //
-// Data path per wave and 16-token block, three blocks in flight:
+// Data path per wave and 16-token block:
 //   K : 16-byte global loads straight into the MFMA A layout (registers);
 //   V : coalesced 16-byte global loads -> per-wave LDS staging (rows padded
 //       to 272 B) -> ds_read_b64_tr_b16 transposing reads = V^T A operand;
 //   Q : staged once per piece in LDS, read as the B operand.
-// A three-stage register ring holds the K/V loads of the next blocks; each
-// stage's K is refilled as soon as S^T has consumed it and its V as soon as
-// it is staged, so every wave keeps about two blocks of loads in flight.
+// A register ring (one block deep for up to 32 rows, two for 48) holds the
+// K/V loads of the wave's next blocks; each stage's K is refilled as soon as
+// S^T has consumed it and its V as soon as it is staged in LDS.
 //
 // Work split.  The host planner cuts the stream of (segment, 16-token block)
 // work into contiguous ranges of near-equal cost, one per workgroup
