@@ -294,3 +294,54 @@ def test_plan_respects_kernel_limits(lib):
     p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
     assert len(p["pieces"]) == 8 and len(p["combines"]) == 0
+
+
+def _attention_with_plan(lib, words, hq=32, hkv=8, bt_stride=4096):
+    """Call nsd_paged_attention with host buffers standing in for device ones.
+
+    Only the host-side plan checks run: every call here must be rejected
+    before any HIP call (a plan that passes would fail at the launch)."""
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    buf = np.zeros(1 << 16, np.uint8)  # 16-byte aligned stand-in pointer
+    p = buf.ctypes.data + (-buf.ctypes.data) % 16
+    ws = np.zeros(1 << 22, np.uint8)
+    wp = ws.ctypes.data + (-ws.ctypes.data) % 16
+    return lib.nsd_paged_attention(p, p, None, p, p, 1000, 2, 0, hq, hkv, 128, 16, p, bt_stride,
+                                   words.ctypes.data_as(i32p), p, wp, ws.size - 16, 128 ** -0.5,
+                                   None, None)
+
+
+@pytest.mark.skipif(Path("/dev/kfd").exists(),
+                    reason="passes host buffers as device pointers: only where no GPU can run it")
+def test_attention_rejects_corrupt_plans(lib):
+    """The kernel claims blocks from the records it is given: the launch
+    checks stride, ring depth, group counts, slots and row counts first."""
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import PIECE_WORDS, plan_words
+
+    sid, sl = [0] * 5 + [1] * 5, [3000 + i for i in range(1, 6)] + [900 + i for i in range(1, 6)]
+    words, _ = plan_words(sid, sl, 32, 8, 128, 16, 2, 4096, 16)
+    h = words[:_lib.PLAN_HEADER_WORDS]
+    op = int(h[_lib.PLAN_OFF_PIECES])
+    split = next(i for i in range(int(h[_lib.PLAN_PIECES]))
+                 if words[op + PIECE_WORDS * i + 3] >= 0)  # a piece with a partial slot
+
+    def corrupt(idx, value):
+        w = words.copy()
+        w[idx] = value
+        return w
+
+    cases = [
+        (corrupt(_lib.PLAN_RING_STAGES, 3), "header"),
+        (corrupt(_lib.PLAN_PIECE_STRIDE, 0), "header"),
+        (corrupt(_lib.PLAN_PIECES, int(h[_lib.PLAN_PIECES]) + 1), "header"),
+        (corrupt(op + 11, words[op + 11] + 1), "piece 0"),                      # group count
+        (corrupt(op + 2, 4096 * 2), "piece 0"),                                 # past the block table row
+        (corrupt(op + 5, 64), "piece 0"),                                       # q_len * gqa > rows_max
+        (corrupt(op + PIECE_WORDS * split + 3, int(h[_lib.PLAN_SLOTS])), f"piece {split}"),
+        (corrupt(op, 8), "piece 0"),                                            # kv head
+    ]
+    for w, where in cases:
+        rc = _attention_with_plan(lib, w)
+        assert rc == 1, (where, rc, _lib.last_error())
+        assert "corrupt plan" in _lib.last_error() and where in _lib.last_error()
