@@ -6,10 +6,15 @@ resident in HBM.  Steps cycle ``cur_layer`` over all 36 layers so the
 ~144 MB per-layer working set cannot stay in the 256 MB Infinity Cache.
 The timed steps are replayed from a HIP graph of one pass over the layers
 (no host launch overhead inside the timed region), timed with HIP events
-on the stream the kernels run on.  The fused prologue (QK-RMSNorm + RoPE +
-KV store) is timed alone and together with the attention.  A secondary
-entry measures Draft decode (Qwen3-0.6B shape, B=64).  The CPU baseline
-times the numpy oracle on the same inputs on this host's cores.
+on the stream the kernels run on: the mean over all timed calls is the
+headline, and the per-replay median / p10 / p90 and a same-layer "hot"
+figure (every call on layer 0, so its blocks stay cached) are reported as
+diagnostics.  The fused prologue (QK-RMSNorm + RoPE + KV store) is timed
+alone and together with the attention.  Secondary entries measure Draft
+decode (Qwen3-0.6B shape, B=64), ragged long-context verify (q_len=9,
+contexts log-U[1024, 32768]) and the small 4-request decode case.  The CPU
+baseline times the numpy oracle on the same inputs on this host's cores,
+median per layer call, for the headline and every secondary workload.
 
 Prints one JSON line (see ``--help``).
 """
@@ -32,19 +37,24 @@ HBM_PEAK_GBPS = 8000.0
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=720, help="timed layer calls (multiple of the layer count)")
+    p.add_argument("--steps", type=int, default=1440, help="timed layer calls (multiple of the layer count)")
     p.add_argument("--warmup", type=int, default=72)
     p.add_argument("--workload", default="target_verify")
-    p.add_argument("--secondary", default="draft_decode", help="second workload ('' to skip)")
+    p.add_argument("--secondary", default="draft_decode,ragged_verify,cpu_plumbing",
+                   help="comma-separated workloads measured beside the headline ('' to skip)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
+    p.add_argument("--other-cpu-seconds", type=float, default=4.0,
+                   help="bound on CPU oracle time for each secondary workload")
     return p.parse_args()
 
 
-def _time_graph(fn, stream, reps: int, wreps: int) -> float:
-    """Capture fn() in a HIP graph on `stream`; µs per replay, timed with HIP
-    events recorded on that same stream around `reps` back-to-back replays."""
+def _time_graph(fn, stream, reps: int, wreps: int):
+    """Capture fn() in a HIP graph on `stream` and replay it `reps` times
+    back to back after `wreps` untimed replays.  HIP events recorded on that
+    same stream before the first timed replay and after each one give the
+    mean µs per replay (first to last event) and the per-replay durations."""
     import torch
 
     fn()  # plans, kernel attributes: everything a capture must not do
@@ -54,17 +64,27 @@ def _time_graph(fn, stream, reps: int, wreps: int) -> float:
         with torch.cuda.graph(graph, stream=stream):
             fn()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     with torch.cuda.stream(stream):
         for _ in range(wreps):
             graph.replay()
-        start.record(stream)
-        for _ in range(reps):
+        events[0].record(stream)
+        for i in range(reps):
             graph.replay()
-        end.record(stream)
+            events[i + 1].record(stream)
     torch.cuda.synchronize()
     del graph
-    return start.elapsed_time(end) * 1e3 / reps
+    per = [events[i].elapsed_time(events[i + 1]) * 1e3 for i in range(reps)]
+    return events[0].elapsed_time(events[reps]) * 1e3 / reps, per
+
+
+def _spread(per_replay, calls_per_replay: int) -> dict:
+    """Median, p10 and p90 of µs per layer call over the timed replays."""
+    import numpy as np
+
+    x = np.asarray(per_replay, dtype=np.float64) / calls_per_replay
+    p10, p50, p90 = np.percentile(x, (10, 50, 90))
+    return {"median": float(p50), "p10": float(p10), "p90": float(p90), "replays": len(x)}
 
 
 def measure(name: str, seed: int, steps: int, warmup: int):
@@ -113,13 +133,21 @@ def measure(name: str, seed: int, steps: int, warmup: int):
                                st, layer, cos, sin)
             paged_attention(qp, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o)
 
+    def hot_pass():
+        for _ in range(L):
+            paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, 0, o)
+
     stream = torch.cuda.Stream()
     reps, wreps = max(1, steps // L), max(1, warmup // L)
     t0 = time.perf_counter()
-    us = _time_graph(attn_pass, stream, reps, wreps) / L
+    us, per = _time_graph(attn_pass, stream, reps, wreps)
+    us /= L
     wall = time.perf_counter() - t0
-    us_pro = _time_graph(prologue_pass, stream, reps, wreps) / L
-    us_layer = _time_graph(layer_pass, stream, reps, wreps) / L
+    us_pro, per_pro = _time_graph(prologue_pass, stream, reps, wreps)
+    us_layer, per_layer = _time_graph(layer_pass, stream, reps, wreps)
+    # Diagnostic only: every call reads layer 0, whose blocks then stay in
+    # the 256 MB Infinity Cache between calls.
+    us_hot, _ = _time_graph(hot_pass, stream, reps, wreps)
     nbytes = w.algorithmic_bytes()
     gbps = nbytes / (us * 1e-6) / 1e9
     plan = st.attn_plan
@@ -137,10 +165,14 @@ def measure(name: str, seed: int, steps: int, warmup: int):
         "kv_tokens": w.kv_tokens(),
         "plan_workers": int(plan.host[5]),
         "plan_rows_max": plan.rows_max,
-        "prologue_us": us_pro,
+        "us_per_layer_call_spread": _spread(per, L),
+        "hot_same_layer_us": us_hot / L,
+        "prologue_us": us_pro / L,
+        "prologue_us_spread": _spread(per_pro, L),
         "prologue_bytes": w.prologue_bytes(),
-        "prologue_gbps": w.prologue_bytes() / (us_pro * 1e-6) / 1e9,
-        "prologue_plus_attention_us": us_layer,
+        "prologue_gbps": w.prologue_bytes() / (us_pro / L * 1e-6) / 1e9,
+        "prologue_plus_attention_us": us_layer / L,
+        "prologue_plus_attention_us_spread": _spread(per_layer, L),
     }
     return res, w
 
@@ -222,7 +254,19 @@ def cpu_baseline(w, budget_s: float):
         "kind": "port",
         "sample": f"{len(times)} layer calls of {w.spec.name} (one layer, same seeded inputs), "
                   f"numpy fp32 oracle, median",
+        "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -252,9 +296,14 @@ def main():
     spec = w.spec
     del w
     torch.cuda.empty_cache()
-    secondary = None
-    if args.secondary:
-        secondary, w2 = measure(args.secondary, args.seed, args.steps, args.warmup)
+    secondary = {}
+    for name in filter(None, args.secondary.split(",")):
+        r2, w2 = measure(name, args.seed, args.steps, args.warmup)
+        print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
+              f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+        if args.cpu_baseline_seconds > 0:
+            r2["cpu_baseline"] = cpu_baseline(w2, args.other_cpu_seconds)
+        secondary[name] = r2
         del w2
         torch.cuda.empty_cache()
     line = {
