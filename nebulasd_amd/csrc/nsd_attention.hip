@@ -21,16 +21,19 @@
 //   V : coalesced 16-byte global loads -> per-wave LDS staging (rows padded
 //       to 272 B) -> ds_read_b64_tr_b16 transposing reads = V^T A operand;
 //   Q : staged once per piece in LDS, read as the B operand.
-// A register ring (one block deep for up to 32 rows, two for 48) holds the
-// K/V loads of the wave's next blocks; each stage's K is refilled as soon as
-// S^T has consumed it and its V as soon as it is staged in LDS.
+// A one-block register ring holds the K/V loads of the wave's next block;
+// its K is refilled as soon as S^T has consumed it and its V as soon as it
+// is staged in LDS.  Eight waves per compute unit (two per SIMD) keep eight
+// blocks in flight; the 64-row shape spills a few registers that only the
+// per-piece code touches.
 //
 // Work split.  The host planner cuts the stream of (segment, 16-token block)
 // work into contiguous ranges of near-equal cost, one per workgroup
 // ("worker"), and there is one workgroup per compute unit.  The workgroup's
 // waves claim its range a group of ring-depth blocks at a time from a
 // counter in LDS, so a wave that streams faster takes more groups, and merge
-// their softmax states through LDS at the end of each piece.  Segments cut
+// their softmax states through LDS at the end of each piece (in two rounds
+// of 64 dims when all eight waves' states for 48 or 64 rows would not fit).  Segments cut
 // across workers write fp32 partials (normalised O, log2-sum-exp); the
 // workgroup that writes a segment's last partial merges them in the same
 // launch.
@@ -102,13 +105,24 @@ struct Tune {
   static constexpr int waves = attn_waves(NT);
 };
 
-// LDS byte sizes: Q rows, then max(per-wave V staging, one-round wave merge).
+// LDS byte sizes: Q rows, then max(per-wave V staging, wave merge).  The
+// merge passes every wave's fp32 state (NT*16 rows of D dims, plus m and l)
+// through LDS, in one round when it fits beside Q, else in two rounds of
+// D/2 dims each.
+constexpr int kLdsDynMax = 160 * 1024 - 2048;  // a compute unit's LDS less the static arrays
+static_assert(kMaxWorkerPieces * (kPieceWords + 1) * 4 + 4 <= 2048, "static LDS arrays");
 template <int NT>
 constexpr int lds_q_bytes() { return NT * 16 * ROWB; }
 template <int NT>
 constexpr int lds_v_bytes() { return Tune<NT>::waves * BS * ROWB; }
 template <int NT>
-constexpr int lds_merge_bytes() { return Tune<NT>::waves * NT * 16 * (RS + 2) * 4; }
+constexpr int merge_cols() {
+  return lds_q_bytes<NT>() + Tune<NT>::waves * NT * 16 * (RS + 2) * 4 <= kLdsDynMax ? D : D / 2;
+}
+template <int NT>
+constexpr int merge_stride() { return merge_cols<NT>() + 4; }  // floats per merged row
+template <int NT>
+constexpr int lds_merge_bytes() { return Tune<NT>::waves * NT * 16 * (merge_stride<NT>() + 2) * 4; }
 // At least half the LDS of a compute unit, so that one workgroup holds a
 // compute unit: its waves then share the unit's work through the claims.
 constexpr int kLdsHalfCu = 80 * 1024 + 16;
@@ -119,6 +133,9 @@ constexpr size_t lds_bytes() {
                                             : lds_merge_bytes<NT>());
   return need > kLdsHalfCu ? need : kLdsHalfCu;
 }
+static_assert(lds_bytes<1>() <= kLdsDynMax && lds_bytes<2>() <= kLdsDynMax &&
+                  lds_bytes<3>() <= kLdsDynMax && lds_bytes<4>() <= kLdsDynMax,
+              "attention LDS exceeds a compute unit");
 
 // Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time unrolled).
 template <int N, typename F, int... I>
@@ -226,8 +243,10 @@ void paged_attn_kernel(AttnArgs a) {
   __shared__ int s_claim;                   // first group of blocks nobody has claimed
   lds_char* smem = (lds_char*)smem_raw;
   lds_char* s_q = smem;                                   // [NT*16][ROWB]
-  float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [NW][NT*16][RS] (aliases V)
-  float* s_ml = s_acc + NW * NT * 16 * RS;                // merge: [NW][2][NT*16]
+  constexpr int MC = merge_cols<NT>();     // dims merged per round
+  constexpr int MS = merge_stride<NT>();
+  float* s_acc = (float*)(smem_raw + lds_q_bytes<NT>());  // merge: [NW][NT*16][MS] (aliases V)
+  float* s_ml = s_acc + NW * NT * 16 * MS;                // merge: [NW][2][NT*16]
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -501,38 +520,42 @@ void paged_attn_kernel(AttnArgs a) {
       l[j] += __shfl_xor(l[j], 32, kWave);
     }
 
-    // Merge the waves' states in one round: every wave writes its live rows
-    // (acc, m, l; empty if it took no group of the piece) to LDS, then all
-    // threads combine them, four dims per thread and step, and write the
-    // fp16 output (or the fp32 partial).
+    // Merge the waves' states through LDS, D/MC rounds of MC dims: every
+    // wave writes its live rows (acc, m, l; empty if it took no group of the
+    // piece), then all threads combine them, four dims per thread and step,
+    // and write the fp16 output (or the fp32 partial).
     __syncthreads();  // every wave is done with its V staging (aliased below) and Q
     if (pc + 1 < n_pc) store_q(pc + 1, qv);
-    {
-      float* ma = s_acc + wave * NT * 16 * RS;
-      float* mm = s_ml + wave * 2 * NT * 16;
+    const int slot = rec(pc, kPieceSlot), row_start = rec(pc, kPieceRowStart);
+    const int h = rec(pc, kPieceHead);
+    const __amdgpu_buffer_rsrc_t rpart =
+        raw_buffer(a.part_o + (int64_t)(slot < 0 ? 0 : slot) * a.rows_max * D,
+                   (uint32_t)a.rows_max * D * 4);
+    static_for<D / MC>([&](auto round) {
+      constexpr int r = decltype(round)::value;
+      constexpr int MT = MC / 16;  // acc tiles per round
+      if (r > 0) __syncthreads();  // every thread has read the previous round
+      {
+        float* ma = s_acc + wave * NT * 16 * MS;
+        float* mm = s_ml + wave * 2 * NT * 16;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int n = 16 * j + lr;
-        if (n < n_rows) {
+        for (int j = 0; j < NT; ++j) {
+          const int n = 16 * j + lr;
+          if (n < n_rows) {
 #pragma unroll
-          for (int mt = 0; mt < 8; ++mt)
-            *reinterpret_cast<f32x4*>(ma + n * RS + 16 * mt + 4 * lg) = acc[j][mt];
-          if (lg == 0) {
-            mm[n] = m[j];
-            mm[NT * 16 + n] = l[j];
+            for (int mt = 0; mt < MT; ++mt)
+              *reinterpret_cast<f32x4*>(ma + n * MS + 16 * mt + 4 * lg) = acc[j][r * MT + mt];
+            if (r == 0 && lg == 0) {
+              mm[n] = m[j];
+              mm[NT * 16 + n] = l[j];
+            }
           }
         }
       }
-    }
-    __syncthreads();
-    {
-      const int slot = rec(pc, kPieceSlot), row_start = rec(pc, kPieceRowStart);
-      const int h = rec(pc, kPieceHead);
-      const __amdgpu_buffer_rsrc_t rpart =
-          raw_buffer(a.part_o + (int64_t)(slot < 0 ? 0 : slot) * a.rows_max * D,
-                     (uint32_t)a.rows_max * D * 4);
-      for (int idx = threadIdx.x; idx < n_rows * (D / 4); idx += NTHR) {
-        const int n = idx / (D / 4), c4 = idx % (D / 4);
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < n_rows * (MC / 4); idx += NTHR) {
+        const int n = idx / (MC / 4), c4 = idx % (MC / 4);
+        const int col = r * MC + 4 * c4;
         float mw[NW], lw[NW], M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
@@ -547,7 +570,7 @@ void paged_attn_kernel(AttnArgs a) {
         for (int w = 0; w < NW; ++w) {  // a wave with no block of the piece has m = -inf
           const float f = exp2f(mw[w] - M_use);
           L += lw[w] * f;
-          ov += *reinterpret_cast<const f32x4*>(s_acc + (w * NT * 16 + n) * RS + 4 * c4) * f;
+          ov += *reinterpret_cast<const f32x4*>(s_acc + (w * NT * 16 + n) * MS + 4 * c4) * f;
         }
         const float inv = L > 0.f ? 1.f / L : 0.f;
         ov *= inv;
@@ -556,16 +579,16 @@ void paged_attn_kernel(AttnArgs a) {
         const float lse2 = L > 0.f ? M + __log2f(L) : -INFINITY;
         if (slot < 0) {
           f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
-          *reinterpret_cast<f16x4*>(a.o + orow * D + 4 * c4) = hv;
-          if (c4 == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
+          *reinterpret_cast<f16x4*>(a.o + orow * D + col) = hv;
+          if (col == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
         } else {
-          store_coherent(rpart, ((uint32_t)n * D + 4 * c4) * 4, ov);
-          if (c4 == 0)
+          store_coherent(rpart, ((uint32_t)n * D + col) * 4, ov);
+          if (col == 0)
             __hip_atomic_store(a.part_lse + (int64_t)slot * a.rows_max + n, lse2,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-    }
+    });
   }
 
   // Arrivals of split segments, once every wave's partial stores are

@@ -73,8 +73,10 @@ constexpr int kMaxWorkerPieces = 32;   // pieces one workgroup keeps records of
 
 // Attention kernel shape for groups of up to 16*nt query rows (nt = 1..4):
 // K/V ring depth, which is also the size of a claimed group of blocks, and
-// waves per workgroup (one workgroup per compute unit).
-constexpr int ring_stages(int nt) { return nt == 3 ? 2 : 1; }
-constexpr int attn_waves(int nt) { return nt <= 2 ? 8 : 4; }
+// waves per workgroup (one workgroup per compute unit).  Every shape now
+// streams with eight waves and a one-block ring; the plan still records the
+// depth it was built for, so a kernel built for another depth rejects it.
+constexpr int ring_stages(int /*nt*/) { return 1; }
+constexpr int attn_waves(int /*nt*/) { return 8; }
 
 }  // namespace nsd

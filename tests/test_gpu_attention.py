@@ -80,6 +80,19 @@ def test_attention_chunk_boundaries(gpu, model, q_len):
     check_against_oracle(w, 2, o, lse, f"edges q_len={q_len}")
 
 
+@pytest.mark.parametrize("q_len", [12, 16], ids=["48rows", "64rows"])
+def test_attention_long_contexts_wide_groups(gpu, q_len):
+    """48- and 64-row groups over log-uniform contexts up to 32k: segments cut
+    into pieces whose wave merge runs in two 64-dim rounds and whose fp32
+    partials are combined across workgroups."""
+    w = make_workload("ragged_verify", 1, device=gpu, num_layers=2, q_len=q_len)
+    o, lse, st = run_attention(w, 1)
+    assert st.attn_plan.host[6] > 0, "expected split segments"
+    check_against_oracle(w, 1, o, lse, f"ragged q_len={q_len}")
+    del w
+    torch.cuda.empty_cache()
+
+
 def test_attention_every_layer_and_repeatable(gpu):
     """Every layer checks against the oracle; a repeated call agrees to within
     fp32 summation-order rounding (waves claim blocks and merge in the order

@@ -73,9 +73,9 @@ MAX_WORKER_PIECES, MIN_PIECE_BLOCKS, PIECE_COST = 32, 4, 24
 
 
 def ring_stages(rows_max):
-    """Blocks per claimed group for groups of up to rows_max query rows."""
-    nt = (rows_max + 15) // 16
-    return 2 if nt == 3 else 1
+    """Blocks per claimed group for groups of up to rows_max query rows
+    (every shape streams with a one-block ring)."""
+    return 1
 
 
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
