@@ -178,6 +178,29 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
                         void* workspace, int64_t workspace_bytes, float softmax_scale,
                         int32_t* status, void* stream);
 
+/*
+ * Prefill (prompt) attention, causal within each prompt of a packed batch.
+ * Replaces flash_attn_varlen_func
+ * (swiftLLM/swiftllm/worker/layers/transformer_layer.py:7-32, called at
+ * :151-164 with cu_seqlens_q == cu_seqlens_k and causal=True) and the Triton
+ * prefill_attention (swiftLLM/swiftllm/worker/kernels/prefill_attn.py:10-140):
+ * prompt s holds tokens [cu_seqlens[s], cu_seqlens[s+1]) of q [T, Hq, d],
+ * k and v [T, Hkv, d]; its position i, q-head qh attends positions 0..i in
+ * kv head qh / (Hq/Hkv) with scores q.k * softmax_scale, and o [T, Hq, d]
+ * gets the softmax-weighted sum of V (fp16 out, fp32 math).  If lse != NULL
+ * it also writes ln(sum exp(score)) as fp32 [T, Hq].
+ * cu_seqlens: device int32 [n_seqs + 1], non-decreasing; a prompt's end past
+ * total_tokens is cut there (the reference's last prompt ends at the
+ * forward's token count and is cut by slicing q[:num_prefill_tokens],
+ * model.py:412-415).  max_seqlen bounds every prompt's length: a longer
+ * prompt, a negative start or a decreasing pair sets NSD_STATUS_BAD_SEQ and
+ * is not (fully) computed.  Hq/Hkv must divide 256.
+ */
+int nsd_prefill_attention(const void* q, const void* k, const void* v, void* o, float* lse,
+                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
+                          int64_t total_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                          float softmax_scale, int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

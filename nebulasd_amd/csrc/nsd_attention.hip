@@ -55,11 +55,6 @@ constexpr int ROWB = D * 2 + 16;     // LDS bytes per staged fp16 row (padded: 1
 constexpr int RS = D + 4;            // LDS row stride (floats) for the wave merge
 constexpr float kLn2 = 0.69314718055994531f;
 
-typedef __attribute__((address_space(3))) char lds_char;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
-typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 
 struct AttnArgs {
   const f16* q;            // [R, Hq, D]
@@ -82,12 +77,6 @@ struct AttnArgs {
   float scale_log2;        // softmax_scale * log2(e)
 };
 
-__device__ inline f32x4 mfma_k32(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-__device__ inline f32x4 mfma_k16(f16x4 a, f16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
 
 // Worker id of this workgroup: hardware dispatches workgroup i to XCD i % 8,
 // so consecutive workers (which share segments) land on the same XCD/L2.
@@ -137,22 +126,7 @@ static_assert(lds_bytes<1>() <= kLdsDynMax && lds_bytes<2>() <= kLdsDynMax &&
                   lds_bytes<3>() <= kLdsDynMax && lds_bytes<4>() <= kLdsDynMax,
               "attention LDS exceeds a compute unit");
 
-// Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time unrolled).
-template <int N, typename F, int... I>
-__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ inline void static_for(F&& f) {
-  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
 
-// Transposing LDS read: lane j of each 16-lane group receives, in slot m,
-// 16-bit element (j % 4) of the 8 bytes addressed by lane 4*m + j/4.
-__device__ inline f16x4 ds_read_tr16(const lds_char* p) {
-  fp16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)p);
-  return __builtin_bit_cast(f16x4, t);
-}
 
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
 // other inside a kernel).  They are written and read with device-scope (sc1)

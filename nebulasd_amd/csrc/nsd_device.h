@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "nsd_common.h"
 
 namespace nsd {
@@ -35,5 +38,38 @@ inline int launch_status(const char* what) {
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+
+// v_mfma_f32_16x16x32_f16: lane (i = lane % 16, g = lane / 16) holds
+// A[i][8g .. 8g+7] and B[8g .. 8g+7][i]; it receives C[4g .. 4g+3][i].
+__device__ inline f32x4 mfma_k32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_16x16x16_f16: as above with k = 16 (A[i][4g .. 4g+3]).
+__device__ inline f32x4 mfma_k16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Transposing LDS read: lane j of each 16-lane group receives, in slot m,
+// 16-bit element (j % 4) of the 8 bytes addressed by lane 4*m + j/4.
+__device__ inline f16x4 ds_read_tr16(const lds_char* p) {
+  fp16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)p);
+  return __builtin_bit_cast(f16x4, t);
+}
+
+// Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time unrolled).
+template <int N, typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
 
 }  // namespace nsd

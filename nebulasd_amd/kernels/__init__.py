@@ -2,9 +2,10 @@
 
 from .kvcache_mgmt import store_kvcache
 from .paged_attn import paged_attention
+from .prefill_attn import flash_attn_varlen_func, prefill_attention
 from .prologue import qk_norm_rope_store
 from .rmsnorm import rmsnorm_inplace
 from .rotary_emb import rotary_embedding_inplace
 
 __all__ = ["paged_attention", "store_kvcache", "rotary_embedding_inplace", "rmsnorm_inplace",
-           "qk_norm_rope_store"]
+           "qk_norm_rope_store", "flash_attn_varlen_func", "prefill_attention"]

@@ -9,6 +9,7 @@ the same contexts, block tables and tensors on every machine.
 
 from __future__ import annotations
 
+import itertools
 import math
 from dataclasses import dataclass, field
 
@@ -183,3 +184,89 @@ def make_workload(spec: WorkloadSpec | str, seed: int = 0, device="cuda",
     q.normal_(0.0, spec.scale, generator=dgen)
     return Workload(spec, seed, ctxs, seq_ids, seq_lens, bt.to(dev), q, k_cache, v_cache,
                     extra={"poison_block": poison})
+
+
+# --------------------------------------------------------------------------
+# Prefill (prompt) attention workloads
+# --------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class PrefillSpec:
+    name: str
+    model: dict
+    batch: int
+    lens: tuple                 # ("uniform", lo, hi): prompt lengths
+    scale: float = 1.0          # std of Q/K/V
+
+    @property
+    def num_q_heads(self) -> int:
+        return self.model["num_attention_heads"]
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.model["num_key_value_heads"]
+
+    @property
+    def num_layers(self) -> int:
+        return self.model["num_hidden_layers"]
+
+    @property
+    def head_dim(self) -> int:
+        return self.model.get("head_dim", self.model["hidden_size"] // self.num_q_heads)
+
+
+PREFILL_SPECS = {
+    # One prefill chunk of the speculative loop: 16 prompts of U[128, 1024] tokens.
+    "prefill_target": PrefillSpec("prefill_target", QWEN3_8B, 16, ("uniform", 128, 1024)),
+    "prefill_draft": PrefillSpec("prefill_draft", QWEN3_0_6B, 16, ("uniform", 128, 1024)),
+}
+
+
+@dataclass
+class PrefillWorkload:
+    spec: PrefillSpec
+    seed: int
+    lens: list                   # prompt lengths
+    cu_seqlens: torch.Tensor     # [batch + 1] int32 (device)
+    q: torch.Tensor              # [tokens, Hq, d] fp16
+    k: torch.Tensor              # [tokens, Hkv, d] fp16
+    v: torch.Tensor
+
+    @property
+    def tokens(self) -> int:
+        return sum(self.lens)
+
+    def flops(self) -> int:
+        """2 flops per multiply-add of QK^T and PV over the causal triangle."""
+        s = self.spec
+        return sum(4 * s.num_q_heads * s.head_dim * n * (n + 1) // 2 for n in self.lens)
+
+    def algorithmic_bytes(self) -> int:
+        """q, k, v read once and o written once."""
+        s = self.spec
+        return self.tokens * (2 * s.num_q_heads + 2 * s.num_kv_heads) * s.head_dim * 2
+
+
+def make_prefill_workload(spec: PrefillSpec | str, seed: int = 0, device="cuda",
+                          lens: list | None = None, model: dict | None = None) -> PrefillWorkload:
+    """Seeded prompts of ``spec`` (or the given ``lens`` / ``model`` shape) on ``device``."""
+    if isinstance(spec, str):
+        spec = PREFILL_SPECS[spec]
+    if model is not None or lens is not None:
+        spec = PrefillSpec(spec.name, model or spec.model, len(lens) if lens is not None else spec.batch,
+                           spec.lens, spec.scale)
+    gen = torch.Generator().manual_seed(seed)
+    if lens is None:
+        _, lo, hi = spec.lens
+        lens = torch.randint(lo, hi + 1, (spec.batch,), generator=gen).tolist()
+    lens = [int(n) for n in lens]
+    dev = torch.device(device)
+    cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32, device=dev)
+    t = sum(lens)
+    dgen = torch.Generator(device=dev).manual_seed(seed + 2000)
+    q = torch.empty((t, spec.num_q_heads, spec.head_dim), dtype=torch.float16, device=dev)
+    k = torch.empty((t, spec.num_kv_heads, spec.head_dim), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    for x in (q, k, v):
+        x.normal_(0.0, spec.scale, generator=dgen)
+    return PrefillWorkload(spec, seed, lens, cu, q, k, v)

@@ -28,6 +28,12 @@ How each function is pinned (see ``tests/test_oracle.py``):
 * ``paged_attention_two_phase`` -- equality with the unsplit
   ``paged_attention`` for several seq_block_size values (the split-KV
   combine must not depend on the partition).
+* ``prefill_attention`` -- ``torch.nn.functional.scaled_dot_product_attention``
+  with ``is_causal=True`` per prompt after ``repeat_interleave`` of K/V
+  (the reference's own formulation, library routine), a pure-Python brute
+  force on tiny inputs, the closed forms position 0 -> v_0 and identical
+  keys -> running mean of V, and the identity prompt = verify group with
+  ctx 0 and q_len = prompt length under the pinned ``paged_attention``.
 """
 
 from __future__ import annotations
@@ -54,6 +60,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_two_phase",
     "reference_seq_block_size",
+    "prefill_attention",
 ]
 
 LOG2E = 1.4426950408889634
@@ -353,4 +360,48 @@ def paged_attention_two_phase(q, k_cache, v_cache, block_table, seq_ids, seq_len
             w = np.exp2(np.asarray(lses) - mx)
             o[r, qh] = (w[:, None] * np.asarray(mids)).sum(0) / w.sum()
             lse[r, qh] = (math.log2(w.sum()) + mx) * LN2
+    return o, lse
+
+
+# --------------------------------------------------------------------------
+# Prefill attention
+# --------------------------------------------------------------------------
+
+def prefill_attention(q, k, v, cu_seqlens, softmax_scale=None, dtype=np.float64):
+    """Causal attention within each prompt of a packed batch, natural-log LSE.
+
+    swiftLLM/swiftllm/worker/layers/transformer_layer.py:7-32 (the
+    flash_attn_varlen_func the layer calls at :151-164 with
+    cu_seqlens_q = cu_seqlens_k and causal=True): prompt i is tokens
+    ``[cu[i], cu[i+1])``; K/V are repeated per q-head (:20-23, q-head qh
+    reads kv head ``qh // (Hq/Hkv)``) and each position attends positions
+    ``0..itself`` (``scaled_dot_product_attention(is_causal=True)``, :25-29).
+    The Triton prefill_attention (K/prefill_attn.py:10-99) computes the same.
+
+    ``q``: [T, Hq, d]; ``k``, ``v``: [T, Hkv, d].  Returns (o [T, Hq, d],
+    lse [T, Hq]) in ``dtype``.
+    """
+    tokens, hq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    if softmax_scale is None:
+        softmax_scale = d ** -0.5
+    cu = [int(x) for x in cu_seqlens]
+    o = np.zeros((tokens, hq, d), dtype=dtype)
+    lse = np.zeros((tokens, hq), dtype=dtype)
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        n = s1 - s0
+        if n <= 0:
+            continue
+        qq = q[s0:s1].astype(dtype).transpose(1, 0, 2)          # [Hq, n, d]
+        kk = np.repeat(k[s0:s1].astype(dtype).transpose(1, 0, 2), g, axis=0)
+        vv = np.repeat(v[s0:s1].astype(dtype).transpose(1, 0, 2), g, axis=0)
+        sc = np.matmul(qq, kk.transpose(0, 2, 1)) * dtype(softmax_scale)   # [Hq, n, n]
+        causal = np.arange(n)[None, :] > np.arange(n)[:, None]
+        sc = np.where(causal[None], -np.inf, sc)
+        m = sc.max(axis=-1, keepdims=True)
+        p = np.exp(sc - m)
+        den = p.sum(axis=-1, keepdims=True)
+        o[s0:s1] = (np.matmul(p, vv) / den).transpose(1, 0, 2)
+        lse[s0:s1] = (np.log(den) + m)[..., 0].T
     return o, lse

@@ -306,3 +306,152 @@ def test_pins_reject_planted_mistakes():
     # (5) LSE in log2 instead of ln
     o, l = oracle.paged_attention(q, kc, vc, bt, sids, lens, layer=1)
     assert _pin_rejects(q, kc, vc, bt, sids, lens, o, l / oracle.LN2)
+
+
+# ---------------------------------------------------------------- prefill attention
+
+def _prefill_case(seed=0, hq=8, hkv=2, d=32, lens=(1, 5, 16, 33, 70)):
+    rng = np.random.default_rng(seed)
+    t = sum(lens)
+    q = rng.standard_normal((t, hq, d)).astype(np.float16)
+    k = rng.standard_normal((t, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((t, hkv, d)).astype(np.float16)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    return q, k, v, cu
+
+
+def prefill_sdpa_reference(q, k, v, cu, scale=None):
+    """The reference's flash_attn_varlen_func (transformer_layer.py:7-32) in
+    float64: per prompt, K/V repeat_interleave'd to the q-heads, then torch
+    SDPA with is_causal=True; LSE from torch.logsumexp over the causal scores."""
+    hq, d = q.shape[1], q.shape[2]
+    scale = d ** -0.5 if scale is None else scale
+    Q, K, V = (torch.from_numpy(x).double() for x in (q, k, v))
+    os, ls = [], []
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        qi = Q[s0:s1].transpose(0, 1).unsqueeze(0)
+        ki = K[s0:s1].transpose(0, 1).unsqueeze(0)
+        vi = V[s0:s1].transpose(0, 1).unsqueeze(0)
+        ki = ki.repeat_interleave(hq // ki.shape[1], dim=1)
+        vi = vi.repeat_interleave(hq // vi.shape[1], dim=1)
+        o = torch.nn.functional.scaled_dot_product_attention(qi, ki, vi, is_causal=True, scale=scale)
+        n = s1 - s0
+        sc = (qi @ ki.transpose(-1, -2)) * scale
+        sc = sc.masked_fill(~torch.ones(n, n, dtype=torch.bool).tril(), float("-inf"))
+        os.append(o.squeeze(0).transpose(0, 1).numpy())
+        ls.append(torch.logsumexp(sc, dim=-1).squeeze(0).transpose(0, 1).numpy())
+    return np.concatenate(os), np.concatenate(ls)
+
+
+def test_prefill_matches_sdpa():
+    q, k, v, cu = _prefill_case()
+    o, lse = oracle.prefill_attention(q, k, v, cu)
+    wo, wl = prefill_sdpa_reference(q, k, v, cu)
+    np.testing.assert_allclose(o, wo, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(lse, wl, atol=1e-12, rtol=1e-12)
+
+
+def test_prefill_bruteforce_tiny():
+    q, k, v, cu = _prefill_case(seed=3, hq=4, hkv=2, d=4, lens=(3, 6))
+    o, lse = oracle.prefill_attention(q, k, v, cu)
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        for i in range(s1 - s0):
+            for qh in range(4):
+                kv = qh // 2
+                sc = [sum(float(q[s0 + i, qh, x]) * float(k[s0 + t, kv, x]) for x in range(4)) * 0.5
+                      for t in range(i + 1)]
+                mx = max(sc)
+                e = [math.exp(x - mx) for x in sc]
+                tot = sum(e)
+                for x in range(4):
+                    want = sum(e[t] * float(v[s0 + t, kv, x]) for t in range(i + 1)) / tot
+                    assert abs(o[s0 + i, qh, x] - want) < 1e-12
+                assert abs(lse[s0 + i, qh] - (math.log(tot) + mx)) < 1e-12
+
+
+def test_prefill_closed_forms():
+    q, k, v, cu = _prefill_case(seed=4)
+    o, lse = oracle.prefill_attention(q, k, v, cu)
+    # position 0 of every prompt attends only itself: o = v_0, lse = its score
+    for s0 in cu[:-1]:
+        for qh in range(8):
+            np.testing.assert_allclose(o[s0, qh], v[s0, qh // 4].astype(np.float64), atol=1e-12)
+            want = float(q[s0, qh].astype(np.float64) @ k[s0, qh // 4].astype(np.float64)) * 32 ** -0.5
+            assert abs(lse[s0, qh] - want) < 1e-12
+    # identical keys within a prompt -> running mean of V, lse = s + ln(i+1)
+    k2 = k.copy()
+    s0, s1 = int(cu[4]), int(cu[5])
+    k2[s0:s1] = k[s0][None]
+    o, lse = oracle.prefill_attention(q, k2, v, cu)
+    vv = v[s0:s1].astype(np.float64)
+    run_mean = np.cumsum(vv, axis=0) / np.arange(1, s1 - s0 + 1)[:, None, None]
+    for qh in range(8):
+        np.testing.assert_allclose(o[s0:s1, qh], run_mean[:, qh // 4], atol=1e-12)
+
+
+def test_prefill_equals_verify_group_from_cache():
+    """A prompt is the verify group with ctx 0 and q_len = its length: store its
+    K/V in a paged cache and run the (pinned) paged_attention on rows with
+    seq_lens 1..n."""
+    q, k, v, cu = _prefill_case(seed=5, lens=(40, 70))
+    o, lse = oracle.prefill_attention(q, k, v, cu)
+    hkv, d, bs, layers = 2, 32, 16, 2
+    blocks = 16
+    kc = np.zeros((blocks, layers, hkv, bs, d), np.float16)
+    vc = np.zeros_like(kc)
+    bt = np.random.default_rng(1).permutation(blocks)[:16].reshape(2, 8)
+    lens = [int(n) for n in np.diff(cu)]
+    oracle.store_kvcache_prefill(k, v, kc, vc, bt, [0, 1], lens, 1)
+    sids = [s for s, n in enumerate(lens) for _ in range(n)]
+    sl = [i + 1 for n in lens for i in range(n)]
+    o2, l2 = oracle.paged_attention(q, kc, vc, bt, sids, sl, layer=1)
+    np.testing.assert_allclose(o, o2, atol=1e-12)
+    np.testing.assert_allclose(lse, l2, atol=1e-12)
+
+
+def _prefill_mutant(q, k, v, cu, allowed, scale=None):
+    """Attention of each prompt with a planted mask allowed(i, t) (numpy)."""
+    hq, d = q.shape[1], q.shape[2]
+    g = hq // k.shape[1]
+    scale = d ** -0.5 if scale is None else scale
+    o = np.zeros(q.shape)
+    lse = np.zeros(q.shape[:2])
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        n = s1 - s0
+        ok = np.array([[allowed(i, t, n) for t in range(n)] for i in range(n)])
+        for qh in range(hq):
+            sc = q[s0:s1, qh].astype(np.float64) @ k[s0:s1, qh // g].astype(np.float64).T * scale
+            sc = np.where(ok, sc, -np.inf)
+            m = sc.max(-1, keepdims=True)
+            e = np.exp(sc - m)
+            o[s0:s1, qh] = e @ v[s0:s1, qh // g].astype(np.float64) / e.sum(-1, keepdims=True)
+            lse[s0:s1, qh] = np.log(e.sum(-1)) + m[:, 0]
+    return o, lse
+
+
+def test_prefill_pins_reject_planted_mistakes():
+    q, k, v, cu = _prefill_case(seed=6)
+    wo, wl = prefill_sdpa_reference(q, k, v, cu)
+
+    def rejects(o_bad, l_bad):
+        return not (np.allclose(o_bad, wo, atol=2e-3, rtol=1e-2) and np.allclose(l_bad, wl, atol=1e-4))
+
+    # the planted-mask helper itself reproduces the pin with the right mask
+    assert not rejects(*_prefill_mutant(q, k, v, cu, lambda i, t, n: t <= i))
+    # (1) no causal mask
+    assert rejects(*_prefill_mutant(q, k, v, cu, lambda i, t, n: True))
+    # (2) causal mask one token too wide
+    assert rejects(*_prefill_mutant(q, k, v, cu, lambda i, t, n: t <= i + 1))
+    # (3) diagonal excluded (position 0 keeps itself)
+    assert rejects(*_prefill_mutant(q, k, v, cu, lambda i, t, n: t < i or t == 0))
+    # (4) missing softmax scale
+    assert rejects(*_prefill_mutant(q, k, v, cu, lambda i, t, n: t <= i, scale=1.0))
+    # (5) prompts not separated (one causal sequence over the packed batch)
+    o, l = oracle.prefill_attention(q, k, v, [0, int(cu[-1])])
+    assert rejects(o, l)
+    # (6) GQA mapping qh % Hkv instead of qh // G
+    hq, hkv = 8, 2
+    perm = [(qh % hkv) * (hq // hkv) + qh // hkv for qh in range(hq)]
+    o, l = oracle.prefill_attention(q[:, perm], k, v, cu)
+    inv = np.argsort(perm)
+    assert rejects(o[:, inv], l[:, inv])
