@@ -194,7 +194,7 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
  * forward's token count and is cut by slicing q[:num_prefill_tokens],
  * model.py:412-415).  max_seqlen bounds every prompt's length: a longer
  * prompt, a negative start or a decreasing pair sets NSD_STATUS_BAD_SEQ and
- * is not (fully) computed.  Hq/Hkv must divide 256.
+ * is not (fully) computed.  Hq/Hkv must divide 128.
  */
 int nsd_prefill_attention(const void* q, const void* k, const void* v, void* o, float* lse,
                           const int32_t* cu_seqlens, int n_seqs, int max_seqlen,

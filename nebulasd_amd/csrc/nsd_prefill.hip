@@ -9,10 +9,12 @@
 // prompt attends the prompt's tokens 0..i; q-head h reads kv head
 // h / (Hq/Hkv) (the repeat_interleave of transformer_layer.py:20-23).
 //
-// Work unit: (prompt, kv head, block of P = 256/gqa positions).  The
-// workgroup's 256 query rows are the gqa q-heads of its P positions, packed
-// as row n = position_offset * gqa + head_in_group, so every K/V tile staged
-// in LDS serves all the q-heads that read it.  Each wave owns 16*NTW rows.
+// Work unit: (prompt, kv head, block of P = rows/gqa positions).  The
+// workgroup's query rows (128: four waves of 32) are the gqa q-heads of its
+// P positions, packed as row n = position_offset * gqa + head_in_group, so
+// every K/V tile staged in LDS serves all the q-heads that read it.  Three
+// workgroups share a compute unit, so one's loads and barriers overlap the
+// others' MFMAs.
 //
 //   S^T[token][row] = K[token][:] . Q[row][:]            A = K (LDS), B = Q^T (registers)
 //   O^T[dim][row]  += V^T[dim][token] . P^T[token][row]  A = V^T (LDS), B = P^T (registers)
@@ -26,7 +28,9 @@
 //
 // K/V tiles of 32 tokens are double-buffered in LDS: each tile's global
 // loads are issued before the previous tile's MFMAs and written to the other
-// buffer after them, one barrier per tile.  Workgroups are issued from the
+// buffer after them, one barrier per tile.  A row's running max is raised
+// lazily (only past a margin, after a wave-wide vote), so most tiles need no
+// cross-lane reduction and no rescaling of the accumulators.  Workgroups are issued from the
 // last position block down, so the longest ones (the most tiles under the
 // causal mask) start first; the q-blocks of one (prompt, kv head) are
 // n_seqs*Hkv workgroups apart, which keeps them on one XCD when that count
@@ -37,19 +41,35 @@ namespace nsd {
 namespace {
 
 constexpr int PD = kHeadDim;        // 128
-constexpr int KT = 32;              // tokens per K/V tile
-constexpr int PROWB = PD * 2 + 16;  // LDS bytes per staged token row (16 B bank shift)
-constexpr int kWgRows = 256;        // query rows (position x q-head) per workgroup
+constexpr int PROWB = PD * 2 + 32;  // LDS bytes per staged token row (32 B bank shift: no conflicts)
 constexpr float kLn2f = 0.69314718055994531f;
+// A row's running max is raised only when a tile's scores exceed it by more
+// than this (log2 units): the softmax terms then stay below 2^8, exact after
+// the final normalisation, and most tiles skip rescaling the accumulators.
+constexpr float kLazyMax = 8.f;
 
-template <int NTW>
-struct PrefillShape {
-  static constexpr int waves = kWgRows / (16 * NTW);
-  static constexpr int threads = waves * kWave;
+// Kernel shape: NTW 16-row tiles per wave, NW waves per workgroup, KT tokens
+// per K/V tile, PF tiles of global loads in flight, LAZY running-max raise.
+template <int NTW_, int NW_, int KT_, int PF_, bool LAZY_, bool SP_ = false, int WPE_ = 1>
+struct PrefillCfg {
+  static constexpr int NTW = NTW_, NW = NW_, KT = KT_, PF = PF_;
+  static constexpr bool LAZY = LAZY_, SP = SP_;
+  static constexpr int WPE = WPE_;  // minimum waves per SIMD the register budget must allow
+  static constexpr int rows = NW * 16 * NTW;  // query rows (position x q-head) per workgroup
+  static constexpr int threads = NW * kWave;
   static constexpr int loads = 2 * KT * (PD / 8) / threads;  // 16-byte K/V loads per thread per tile
+  static constexpr int lds_bytes = 2 * 2 * KT * PROWB;       // [buffer][K, V][token][padded row]
   static_assert(loads * threads == 2 * KT * (PD / 8), "tile loads split evenly");
   static_assert((KT * (PD / 8)) % threads == 0, "each load is all-K or all-V");
+  static_assert(KT % 32 == 0 && (PF == 1 || PF == 2), "tile shape");
 };
+
+// The shape every launch uses: 32 rows per wave, four waves, 32-token
+// tiles, three workgroups per compute unit (168 VGPRs).  Measured against
+// 8-wave workgroups (one per CU), 64-token tiles, a second tile in flight,
+// 16- and 64-row waves and the software-pipelined loop, all slower; shapes
+// that spill registers were slowest.
+using PrefillShape = PrefillCfg<2, 4, 32, 1, true, false, 3>;
 
 struct PrefillArgs {
   const f16* q;               // [T, Hq, D]
@@ -61,19 +81,19 @@ struct PrefillArgs {
   int32_t* status;
   int64_t total_tokens;
   int n_seqs, hq, hkv, gqa;
-  int positions;              // P = kWgRows / gqa
+  int positions;              // P = rows per workgroup / gqa
   int max_seqlen;
   int q_blocks;               // ceil(max_seqlen / P)
   float scale_log2;           // softmax_scale * log2(e)
 };
 
-template <int NTW>
-__global__ void __launch_bounds__(PrefillShape<NTW>::threads)
+template <class C>
+__global__ void __launch_bounds__(C::threads) __attribute__((amdgpu_waves_per_eu(C::WPE)))
 prefill_attn_kernel(PrefillArgs a) {
-  using Shape = PrefillShape<NTW>;
-  constexpr int NTHR = Shape::threads;
-  constexpr int LPT = Shape::loads;
-  __shared__ __align__(16) char s_kv[2][2][KT * PROWB];  // [buffer][K, V][token][padded row]
+  constexpr int NTW = C::NTW, KT = C::KT, NTHR = C::threads, LPT = C::loads;
+  constexpr int KH = KT / 16;  // 16-token score tiles per K/V tile
+  extern __shared__ __align__(16) char smem_raw[];
+  lds_char* s_kv = (lds_char*)smem_raw;  // buffer b, K (0) or V (1): s_kv + (2b + kv) * KT * PROWB
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -121,10 +141,16 @@ prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[j][kk] = *reinterpret_cast<const f16x8*>(qp + 32 * kk);
   }
+  // Keep the Q loads ahead of the first tile's: the wait that stores tile 0
+  // then covers them, and the tile loop never waits on Q (a wait inside the
+  // loop would also drain the next tile's loads every iteration).
+  asm volatile("" ::: "memory");
 
-  // K/V tile staging: thread chunk c -> (K or V, token, 16-byte part).
-  u32x4 stage[LPT];
-  auto load_tile = [&](int t) {
+  // K/V tile staging through registers: thread chunk c -> (K or V, token,
+  // 16-byte part); tile u is loaded into stage[u % PF].
+  u32x4 stage[C::PF][LPT];
+  auto load_tile = [&](auto sidx, int t) {
+    constexpr int S = decltype(sidx)::value;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + i * NTHR;
@@ -132,17 +158,18 @@ prefill_attn_kernel(PrefillArgs a) {
       const int tok = (c / (PD / 8)) % KT, part = c % (PD / 8);
       const int tk = min(t * KT + tok, len - 1);  // past the prompt: masked, reads its last row
       const f16* base = kv ? a.v : a.k;
-      stage[i] = *reinterpret_cast<const u32x4*>(base + ((int64_t)(start + tk) * a.hkv + kvh) * PD +
-                                                 part * 8);
+      stage[S][i] = *reinterpret_cast<const u32x4*>(base + ((int64_t)(start + tk) * a.hkv + kvh) * PD +
+                                                    part * 8);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](auto sidx, int buf) {
+    constexpr int S = decltype(sidx)::value;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + i * NTHR;
       const int kv = (i * NTHR) / (KT * (PD / 8));
       const int tok = (c / (PD / 8)) % KT, part = c % (PD / 8);
-      *(lds_u32x4*)((lds_char*)&s_kv[buf][kv][0] + tok * PROWB + part * 16) = stage[i];
+      *(lds_u32x4*)(s_kv + (2 * buf + kv) * KT * PROWB + tok * PROWB + part * 16) = stage[S][i];
     }
   };
 
@@ -157,81 +184,266 @@ prefill_attn_kernel(PrefillArgs a) {
   }
   const float c = a.scale_log2;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
+  // One K/V tile from LDS buffer `buf`: S^T, mask, online softmax, PV.
+  auto compute = [&](int t, int buf) {
     const int t0 = t * KT;
-    if (wave_live && t0 <= wave_last) {  // some row of this wave sees a token of the tile
-      const lds_char* kb = (const lds_char*)&s_kv[buf][0][0];
-      const lds_char* vb = (const lds_char*)&s_kv[buf][1][0];
-      // S^T for the tile's two 16-token halves.
-      f32x4 s[2][NTW];
+    if (!(wave_live && t0 <= wave_last)) return;  // no row of this wave sees a token of the tile
+    const lds_char* kb = s_kv + (2 * buf) * KT * PROWB;
+    const lds_char* vb = kb + KT * PROWB;
+    // (k-steps outermost: KH * NTW independent accumulators between reuses)
+    f32x4 s[KH][NTW];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < KH; ++h)
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) s[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NTW; ++j) s[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const f16x8 kf = *(const lds_f16x8*)(kb + (16 * h + lr) * PROWB + 64 * kk + 16 * lg);
+    for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-          for (int j = 0; j < NTW; ++j) s[h][j] = mfma_k32(kf, qf[j][kk], s[h][j]);
-        }
+      for (int h = 0; h < KH; ++h) {
+        const f16x8 kf = *(const lds_f16x8*)(kb + (16 * h + lr) * PROWB + 64 * kk + 16 * lg);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) s[h][j] = mfma_k32(kf, qf[j][kk], s[h][j]);
       }
-      // Causal mask where the tile reaches the block's positions (it also
-      // hides tokens past the prompt: they lie past every valid row).
-      if (t0 + KT - 1 >= p0) {
+    }
+    // Causal mask where the tile reaches the block's positions (it also
+    // hides tokens past the prompt: they lie past every valid row).
+    if (t0 + KT - 1 >= p0) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < KH; ++h)
 #pragma unroll
-          for (int j = 0; j < NTW; ++j)
+        for (int j = 0; j < NTW; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (t0 + 16 * h + 4 * lg + i > pos_row[j]) s[h][j][i] = -INFINITY;
-      }
-      // Online softmax; P^T in the PV operand layout (tokens 4lg+i, 16+4lg+i).
-      f16x8 pf[NTW];
+          for (int i = 0; i < 4; ++i)
+            if (t0 + 16 * h + 4 * lg + i > pos_row[j]) s[h][j][i] = -INFINITY;
+    }
+    // Online softmax in the exp2 domain.  Each lane checks its own scores
+    // against the running max; only when some lane of the wave exceeds it by
+    // more than kLazyMax are the rows' maxima reduced across the four lane
+    // groups and raised (the common case needs no cross-lane traffic).
+    float mxs[NTW];
+    bool raise = false;
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < KH; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][j][i]);
+      mxs[j] = mx * c;
+      raise |= C::LAZY ? mxs[j] > m[j] + kLazyMax : true;
+    }
+    if (!C::LAZY || __any(raise)) {
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][j][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float m_new = fmaxf(m[j], mx * c);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m[j] - m_use);
-        float ps = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = exp2f(fmaf(s[h][j][i], c, -m_use));
-            ps += p;
-            pf[j][4 * h + i] = (f16)p;
-          }
-        l[j] = l[j] * alpha + ps;
-        m[j] = m_new;
+        mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 16, kWave));
+        mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 32, kWave));
+        const float m_new = fmaxf(m[j], mxs[j]);
+        const float alpha = __builtin_amdgcn_exp2f(m[j] - (m_new == -INFINITY ? 0.f : m_new));
+        l[j] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+        m[j] = m_new;
       }
-      // O^T += V^T . P^T, 16 dims at a time.
-      const lds_char* vsrc = vb + (4 * lg + (lr >> 2)) * PROWB + 8 * (lr & 3);
+    }
+    // P^T in the PV operand layout: k-step ks holds tokens 32ks + 4lg + i and
+    // 32ks + 16 + 4lg + i.
+    f16x8 pf[KT / 32][NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const float m_use = m[j] == -INFINITY ? 0.f : m[j];
+      float ps = 0.f;
+#pragma unroll
+      for (int h = 0; h < KH; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[h][j][i], c, -m_use));
+          ps += p;
+          pf[h / 2][j][4 * (h % 2) + i] = (f16)p;
+        }
+      l[j] += ps;
+    }
+    // O^T += V^T . P^T, 16 dims and 32 tokens per MFMA.
+#pragma unroll
+    for (int ks = 0; ks < KT / 32; ++ks) {
+      const lds_char* vsrc = vb + (32 * ks + 4 * lg + (lr >> 2)) * PROWB + 8 * (lr & 3);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const f16x4 lo = ds_read_tr16(vsrc + 32 * dt);
         const f16x4 hi = ds_read_tr16(vsrc + 16 * PROWB + 32 * dt);
         const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) acc[j][dt] = mfma_k32(vf, pf[j], acc[j][dt]);
+        for (int j = 0; j < NTW; ++j) acc[j][dt] = mfma_k32(vf, pf[ks][j], acc[j][dt]);
       }
     }
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+  };
+
+  if constexpr (C::SP) {
+    // Software pipeline: K runs one tile ahead of V.  While the softmax of
+    // tile t turns its scores into P, the wave issues the score MFMAs of tile
+    // t + 1 (K already in LDS) and the PV MFMAs of tile t, so the matrix
+    // cores and the VALU work at the same time.
+    constexpr int LPK = KT * (PD / 8) / NTHR;  // 16-byte loads per thread of one K or V tile
+    static_assert(LPK * NTHR == KT * (PD / 8), "K/V tile loads split evenly");
+    u32x4 kst[LPK], vst[LPK];
+    auto load_kv = [&](u32x4 (&st)[LPK], const f16* base, int t) {
+#pragma unroll
+      for (int i = 0; i < LPK; ++i) {
+        const int cc = threadIdx.x + i * NTHR;
+        const int tok = cc / (PD / 8), part = cc % (PD / 8);
+        const int tk = min(t * KT + tok, len - 1);  // past the prompt: masked, reads its last row
+        st[i] = *reinterpret_cast<const u32x4*>(base + ((int64_t)(start + tk) * a.hkv + kvh) * PD + part * 8);
+      }
+    };
+    auto store_kv = [&](const u32x4 (&st)[LPK], lds_char* dst) {
+#pragma unroll
+      for (int i = 0; i < LPK; ++i) {
+        const int cc = threadIdx.x + i * NTHR;
+        *(lds_u32x4*)(dst + (cc / (PD / 8)) * PROWB + (cc % (PD / 8)) * 16) = st[i];
+      }
+    };
+    lds_char* kbuf[2] = {s_kv, s_kv + KT * PROWB};
+    lds_char* vbuf[2] = {s_kv + 2 * KT * PROWB, s_kv + 3 * KT * PROWB};
+    auto score = [&](const lds_char* kb, f32x4 (&sc)[KH][NTW]) {
+#pragma unroll
+      for (int h = 0; h < KH; ++h)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) sc[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+        for (int h = 0; h < KH; ++h) {
+          const f16x8 kf = *(const lds_f16x8*)(kb + (16 * h + lr) * PROWB + 64 * kk + 16 * lg);
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) sc[h][j] = mfma_k32(kf, qf[j][kk], sc[h][j]);
+        }
+      }
+    };
+    // Softmax of tile t's scores `sc` and its PV product from `vb`; the score
+    // MFMAs of the next tile (`kb_next` into `sn`) are issued in the same
+    // basic block.
+    auto step = [&](int t, f32x4 (&sc)[KH][NTW], const lds_char* vb, const lds_char* kb_next,
+                    f32x4 (&sn)[KH][NTW]) {
+      const int t0 = t * KT;
+      if (t0 + KT - 1 >= p0) {  // causal mask (also hides tokens past the prompt)
+#pragma unroll
+        for (int h = 0; h < KH; ++h)
+#pragma unroll
+          for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (t0 + 16 * h + 4 * lg + i > pos_row[j]) sc[h][j][i] = -INFINITY;
+      }
+      float mxs[NTW];
+      bool raise = false;
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < KH; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[h][j][i]);
+        mxs[j] = mx * c;
+        raise |= mxs[j] > m[j] + kLazyMax;
+      }
+      if (__any(raise)) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 16, kWave));
+          mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 32, kWave));
+          const float m_new = fmaxf(m[j], mxs[j]);
+          const float alpha = __builtin_amdgcn_exp2f(m[j] - (m_new == -INFINITY ? 0.f : m_new));
+          l[j] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+          m[j] = m_new;
+        }
+      }
+      score(kb_next, sn);
+      f16x8 pf[KT / 32][NTW];
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const float m_use = m[j] == -INFINITY ? 0.f : m[j];
+        float ps = 0.f;
+#pragma unroll
+        for (int h = 0; h < KH; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[h][j][i], c, -m_use));
+            ps += pv;
+            pf[h / 2][j][4 * (h % 2) + i] = (f16)pv;
+          }
+        l[j] += ps;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KT / 32; ++ks) {
+        const lds_char* vsrc = vb + (32 * ks + 4 * lg + (lr >> 2)) * PROWB + 8 * (lr & 3);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const f16x4 lo = ds_read_tr16(vsrc + 32 * dt);
+          const f16x4 hi = ds_read_tr16(vsrc + 16 * PROWB + 32 * dt);
+          const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) acc[j][dt] = mfma_k32(vf, pf[ks][j], acc[j][dt]);
+        }
+      }
+    };
+
+    // Prologue: K(0), V(0), K(1) staged; scores of tile 0.
+    load_kv(kst, a.k, 0);
+    load_kv(vst, a.v, 0);
+    store_kv(kst, kbuf[0]);
+    store_kv(vst, vbuf[0]);
+    if (n_tiles > 1) {
+      load_kv(kst, a.k, 1);
+      store_kv(kst, kbuf[1]);
+    }
     __syncthreads();
+    f32x4 sa[KH][NTW], sb[KH][NTW];
+    score(kbuf[0], sa);
+    __syncthreads();  // every wave has read K(0) before K(2) replaces it
+    // Iteration t: loads of K(t+2), V(t+1); step(t); stores; one barrier.
+    auto iteration = [&](auto par, int t, f32x4 (&sc)[KH][NTW], f32x4 (&sn)[KH][NTW]) {
+      constexpr int B = decltype(par)::value;  // t % 2
+      if (t + 2 < n_tiles) load_kv(kst, a.k, t + 2);
+      if (t + 1 < n_tiles) load_kv(vst, a.v, t + 1);
+      step(t, sc, vbuf[B], kbuf[B ^ 1], sn);  // past the last tile the next scores are unused
+      if (t + 2 < n_tiles) store_kv(kst, kbuf[B]);
+      if (t + 1 < n_tiles) store_kv(vst, vbuf[B ^ 1]);
+      __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      iteration(std::integral_constant<int, 0>{}, t, sa, sb);
+      if (t + 1 < n_tiles) iteration(std::integral_constant<int, 1>{}, t + 1, sb, sa);
+    }
+  } else {
+  // Pipeline: tile t is computed from LDS buffer t % 2 while the loads of
+    // tile t + PF are in flight; tile t + 1 (loaded PF - 1 tiles earlier) goes
+    // to the other buffer after the compute, then one barrier.
+    using std::integral_constant;
+    load_tile(integral_constant<int, 0>{}, 0);
+    if constexpr (C::PF == 2) {
+      if (n_tiles > 1) load_tile(integral_constant<int, 1>{}, 1);
+    }
+    store_tile(integral_constant<int, 0>{}, 0);
+    __syncthreads();
+    auto iteration = [&](auto par, int t) {
+      constexpr int S = decltype(par)::value;  // t % 2
+      if constexpr (C::PF == 1) {
+        if (t + 1 < n_tiles) load_tile(integral_constant<int, 0>{}, t + 1);
+        compute(t, S);
+        if (t + 1 < n_tiles) store_tile(integral_constant<int, 0>{}, S ^ 1);
+      } else {
+        if (t + 2 < n_tiles) load_tile(integral_constant<int, S>{}, t + 2);
+        compute(t, S);
+        if (t + 1 < n_tiles) store_tile(integral_constant<int, S ^ 1>{}, S ^ 1);
+      }
+      __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      iteration(integral_constant<int, 0>{}, t);
+      if (t + 1 < n_tiles) iteration(integral_constant<int, 1>{}, t + 1);
+    }
+
   }
 
   // Normalise and write the valid rows.
@@ -258,12 +470,21 @@ prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
-template <int NTW>
-int launch_prefill(const PrefillArgs& args, hipStream_t stream) {
+template <class C>
+int launch_prefill(PrefillArgs args, hipStream_t stream) {
+  static bool attr_set = false;  // per-process: allow the dynamic LDS once
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<C>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::lds_bytes);
+    if (e != hipSuccess)
+      return fail(NSD_ERR_HIP, "prefill_attention: LDS attribute: %s", hipGetErrorString(e));
+    attr_set = true;
+  }
+  args.positions = C::rows / args.gqa;
+  args.q_blocks = (args.max_seqlen + args.positions - 1) / args.positions;
   const int64_t grid = (int64_t)args.q_blocks * args.n_seqs * args.hkv;
   if (grid > INT32_MAX) return fail(NSD_ERR_UNSUPPORTED, "prefill_attention: grid of %lld workgroups", (long long)grid);
-  hipLaunchKernelGGL(prefill_attn_kernel<NTW>, dim3((unsigned)grid), dim3(PrefillShape<NTW>::threads), 0,
-                     stream, args);
+  hipLaunchKernelGGL(prefill_attn_kernel<C>, dim3((unsigned)grid), dim3(C::threads), C::lds_bytes, stream, args);
   return launch_status("prefill_attention");
 }
 
@@ -281,8 +502,9 @@ extern "C" int nsd_prefill_attention(const void* q, const void* k, const void* v
     return fail(NSD_ERR_INVALID, "prefill_attention: num_q_heads=%d not a multiple of num_kv_heads=%d",
                 num_q_heads, num_kv_heads);
   const int gqa = num_q_heads / num_kv_heads;
-  if (kWgRows % gqa != 0)
-    return fail(NSD_ERR_UNSUPPORTED, "prefill_attention: q-heads per kv head %d must divide %d", gqa, kWgRows);
+  if (PrefillShape::rows % gqa != 0)
+    return fail(NSD_ERR_UNSUPPORTED, "prefill_attention: q-heads per kv head %d must divide %d", gqa,
+                PrefillShape::rows);
   if (n_seqs < 0 || max_seqlen < 0 || total_tokens < 0)
     return fail(NSD_ERR_INVALID, "prefill_attention: negative size");
   if (n_seqs == 0 || max_seqlen == 0 || total_tokens == 0) return NSD_OK;
@@ -303,9 +525,7 @@ extern "C" int nsd_prefill_attention(const void* q, const void* k, const void* v
   args.hq = num_q_heads;
   args.hkv = num_kv_heads;
   args.gqa = gqa;
-  args.positions = kWgRows / gqa;
   args.max_seqlen = max_seqlen;
-  args.q_blocks = (max_seqlen + args.positions - 1) / args.positions;
   args.scale_log2 = softmax_scale * 1.4426950408889634f;
-  return launch_prefill<4>(args, as_stream(stream));
+  return launch_prefill<PrefillShape>(args, as_stream(stream));
 }
