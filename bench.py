@@ -12,9 +12,11 @@ figure (every call on layer 0, so its blocks stay cached) are reported as
 diagnostics.  The fused prologue (QK-RMSNorm + RoPE + KV store) is timed
 alone and together with the attention.  Secondary entries measure Draft
 decode (Qwen3-0.6B shape, B=64), ragged long-context verify (q_len=9,
-contexts log-U[1024, 32768]) and the small 4-request decode case.  The CPU
-baseline times the numpy oracle on the same inputs on this host's cores,
-median per layer call, for the headline and every secondary workload.
+contexts log-U[1024, 32768]) and the small 4-request decode case, and the
+prefill attention of one 16-prompt chunk (prompts U[128, 1024], both model
+shapes) with its MFMA roofline and the reference's per-prompt SDPA loop
+timed beside it.  The CPU baseline times the numpy oracle on the same inputs
+on this host's cores, median per layer call, for every workload.
 
 Prints one JSON line (see ``--help``).
 """
@@ -42,6 +44,8 @@ def parse_args():
     p.add_argument("--workload", default="target_verify")
     p.add_argument("--secondary", default="draft_decode,ragged_verify,cpu_plumbing",
                    help="comma-separated workloads measured beside the headline ('' to skip)")
+    p.add_argument("--prefill", default="prefill_target,prefill_draft",
+                   help="comma-separated prefill-attention workloads ('' to skip)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -177,6 +181,100 @@ def measure(name: str, seed: int, steps: int, warmup: int):
     return res, w
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: float):
+    """Prefill (prompt) attention of workload `name`: µs per layer call from a
+    HIP graph of `calls` back-to-back launches on the same prompts, the
+    reference's per-prompt SDPA loop (transformer_layer.py:7-32) timed the
+    same way on the GPU, and the numpy oracle on the host (bounded)."""
+    import numpy as np
+    import torch
+
+    from nebulasd_amd.kernels import flash_attn_varlen_func
+    from nebulasd_amd.workload import make_prefill_workload
+
+    dev = torch.device("cuda:0")
+    w = make_prefill_workload(name, seed, device=dev)
+    mx = max(w.lens)
+    calls = w.spec.num_layers
+
+    def kernel_pass():
+        for _ in range(calls):
+            flash_attn_varlen_func(w.q, w.k, w.v, w.cu_seqlens, w.cu_seqlens, mx, mx)
+
+    cu = w.cu_seqlens.cpu().tolist()
+    g = w.q.shape[1] // w.k.shape[1]
+
+    def sdpa_pass():  # the reference's loop, fp16 on the GPU
+        outs = []
+        for s0, s1 in zip(cu[:-1], cu[1:]):
+            qi = w.q[s0:s1].transpose(0, 1).unsqueeze(0)
+            ki = w.k[s0:s1].transpose(0, 1).unsqueeze(0).repeat_interleave(g, dim=1)
+            vi = w.v[s0:s1].transpose(0, 1).unsqueeze(0).repeat_interleave(g, dim=1)
+            outs.append(torch.nn.functional.scaled_dot_product_attention(qi, ki, vi, is_causal=True)
+                        .squeeze(0).transpose(0, 1))
+        return torch.cat(outs)
+
+    stream = torch.cuda.Stream()
+    reps, wreps = max(1, steps // calls), max(1, warmup // calls)
+    us, per = _time_graph(kernel_pass, stream, reps, wreps)
+    us /= calls
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sdpa_pass()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        sdpa_pass()
+    e1.record()
+    torch.cuda.synchronize()
+    us_sdpa = e0.elapsed_time(e1) * 1e3 / 5
+    flops = w.flops()
+    tflops = flops / (us * 1e-6) / 1e12
+    res = {
+        "workload": name,
+        "kind": "prefill",
+        "steps": reps * calls,
+        "us_per_layer_call": us,
+        "us_per_layer_call_spread": _spread(per, calls),
+        "prompts": w.lens,
+        "tokens": w.tokens,
+        "flops": flops,
+        "tflops": tflops,
+        "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None},
+        "algorithmic_bytes": w.algorithmic_bytes(),
+        "reference_sdpa_loop_us": us_sdpa,
+        "speedup_vs_sdpa_loop": us_sdpa / us,
+    }
+    if cpu_seconds > 0:
+        import oracle
+        from threadpoolctl import threadpool_info, threadpool_limits
+
+        q, k, v = (x.cpu().numpy() for x in (w.q, w.k, w.v))
+        cores = min(len(os.sched_getaffinity(0)), 16)
+        times = []
+        with threadpool_limits(limits=cores):
+            threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+            t_end = time.perf_counter() + cpu_seconds
+            while True:
+                t0 = time.perf_counter()
+                oracle.prefill_attention(q, k, v, cu, dtype=np.float32)
+                times.append(time.perf_counter() - t0)
+                if time.perf_counter() > t_end or len(times) >= 20:
+                    break
+        res["cpu_baseline"] = {"value": float(np.median(times)) * 1e6, "unit": "us/layer-call",
+                               "cores": int(min(threads, cores)), "kind": "port",
+                               "sample": f"{len(times)} calls of {name}, numpy fp32 oracle, median",
+                               "cpu_model": _cpu_model()}
+    del w
+    torch.cuda.empty_cache()
+    return res
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch for `workload`, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy
@@ -297,6 +395,12 @@ def main():
     del w
     torch.cuda.empty_cache()
     secondary = {}
+    for name in filter(None, args.prefill.split(",")):
+        r2 = measure_prefill(name, args.seed, args.steps, args.warmup, args.other_cpu_seconds
+                             if args.cpu_baseline_seconds > 0 else 0)
+        print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, {r2['tflops']:.0f} TFLOP/s "
+              f"(reference SDPA loop {r2['reference_sdpa_loop_us']:.0f} us)", file=sys.stderr, flush=True)
+        secondary[name] = r2
     for name in filter(None, args.secondary.split(",")):
         r2, w2 = measure(name, args.seed, args.steps, args.warmup)
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "

@@ -7,9 +7,10 @@ this package's gfx950 kernels:
 * decode / verify rows: QK-RMSNorm + RoPE + KV store in one launch
   (``qk_norm_rope_store``), then paged attention, in the order of
   swiftLLM/swiftllm/worker/layers/transformer_layer.py:105-185;
-* prefill: ``rmsnorm_inplace`` on q/k, ``rotary_embedding_inplace`` and the
-  prefill ``store_kvcache``, with per-request causal SDPA for the prompt's
-  attention (transformer_layer.py:7-32);
+* prefill: ``rmsnorm_inplace`` on q/k, ``rotary_embedding_inplace``, the
+  prefill ``store_kvcache`` and the prompts' causal attention in one launch
+  (``flash_attn_varlen_func``, the entry point of transformer_layer.py:7-32
+  and :151-164);
 * the rest of the layer (projections, MLP, norms, lm_head) is plain torch, as
   in the reference (kernels/linear.py:3-12); weights are random (no
   checkpoints are available offline).
@@ -42,8 +43,8 @@ import torch.nn.functional as F
 
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from .infer_state import build_infer_state, rope_cache
-from .kernels import (paged_attention, qk_norm_rope_store, rmsnorm_inplace,
-                      rotary_embedding_inplace, store_kvcache)
+from .kernels import (flash_attn_varlen_func, paged_attention, qk_norm_rope_store,
+                      rmsnorm_inplace, rotary_embedding_inplace, store_kvcache)
 from .speculative import compute_greedy_acceptance
 
 
@@ -113,13 +114,9 @@ class RandomQwen3:
             rmsnorm_inplace(k.view(-1, d), lw["k_norm"], mc.rms_norm_eps)
             rotary_embedding_inplace(q, k, st)
             store_kvcache(k, v, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st, li)
-            o = torch.empty_like(q)
-            for r in range(len(prompts)):
-                s, e = int(starts[r]), int(starts[r + 1])
-                qr = q[s:e].transpose(0, 1).contiguous()
-                kr = k[s:e].repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
-                vr = v[s:e].repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
-                o[s:e] = F.scaled_dot_product_attention(qr, kr, vr, is_causal=True).transpose(0, 1)
+            o = flash_attn_varlen_func(q, k, v, st.prefill_seq_start_locs_with_end,
+                                       st.prefill_seq_start_locs_with_end, st.max_prefill_len,
+                                       st.max_prefill_len, softmax_scale=st.softmax_scale)
             x = x + F.linear(o.view(x.shape[0], -1), lw["wo"])
             x = self._mlp(lw, x)
         last = torch.tensor(starts[1:] - 1, device=dev)
