@@ -195,9 +195,14 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
  * model.py:412-415).  max_seqlen bounds every prompt's length: a longer
  * prompt, a negative start or a decreasing pair sets NSD_STATUS_BAD_SEQ and
  * is not (fully) computed.  Hq/Hkv must divide 128.
+ * seq_order (optional, device int32 [n_seqs]): the prompts longest first (a
+ * permutation of 0..n_seqs-1; any order is correct, this one balances the
+ * shader engines); NULL visits them in order.  An entry outside
+ * [0, n_seqs) sets NSD_STATUS_BAD_SEQ.
  */
 int nsd_prefill_attention(const void* q, const void* k, const void* v, void* o, float* lse,
-                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
+                          const int32_t* cu_seqlens, const int32_t* seq_order, int n_seqs,
+                          int max_seqlen,
                           int64_t total_tokens, int num_q_heads, int num_kv_heads, int head_dim,
                           float softmax_scale, int32_t* status, void* stream);
 

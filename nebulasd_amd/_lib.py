@@ -56,8 +56,8 @@ SIGNATURES = {
                 c_int, c_int, c_int, c_void_p, c_int64, _I32P, c_void_p, c_void_p, c_int64,
                 c_float, c_void_p, c_void_p]),
     "nsd_prefill_attention": (
-        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64,
-                c_int, c_int, c_int, c_float, c_void_p, c_void_p]),
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),
 }
 
 

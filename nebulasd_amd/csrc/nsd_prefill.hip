@@ -78,6 +78,7 @@ struct PrefillArgs {
   f16* o;                     // [T, Hq, D]
   float* lse;                 // [T, Hq] natural log, optional
   const int32_t* cu_seqlens;  // [n_seqs + 1]
+  const int32_t* seq_order;   // [n_seqs] prompts longest first, or null (natural order)
   int32_t* status;
   int64_t total_tokens;
   int n_seqs, hq, hkv, gqa;
@@ -104,7 +105,18 @@ prefill_attn_kernel(PrefillArgs a) {
   const int per_qb = a.n_seqs * a.hkv;
   const int qb = a.q_blocks - 1 - (int)blockIdx.x / per_qb;
   const int item = (int)blockIdx.x % per_qb;
-  const int seq = item / a.hkv, kvh = item - (item / a.hkv) * a.hkv;
+  const int pos = item / a.hkv, kvh = item - pos * a.hkv;
+  // With prompts longest first, a block level's non-empty items are
+  // consecutive (cyclically), so in-order dispatch spreads them over the
+  // shader engines; rotating each level by its index moves the longest
+  // prompts to another engine at every level instead of stacking one
+  // engine's slots with them.
+  const int rank = (pos + qb) % a.n_seqs;
+  const int seq = a.seq_order != nullptr ? a.seq_order[rank] : rank;
+  if (seq < 0 || seq >= a.n_seqs) {
+    if (threadIdx.x == 0) flag_status(a.status, NSD_STATUS_BAD_SEQ);
+    return;
+  }
   const int start = a.cu_seqlens[seq];
   const int end = a.cu_seqlens[seq + 1];
   const int P = a.positions;
@@ -494,7 +506,8 @@ int launch_prefill(PrefillArgs args, hipStream_t stream) {
 using namespace nsd;
 
 extern "C" int nsd_prefill_attention(const void* q, const void* k, const void* v, void* o, float* lse,
-                                     const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
+                                     const int32_t* cu_seqlens, const int32_t* seq_order,
+                                     int n_seqs, int max_seqlen,
                                      int64_t total_tokens, int num_q_heads, int num_kv_heads,
                                      int head_dim, float softmax_scale, int32_t* status, void* stream) {
   if (head_dim != PD) return fail(NSD_ERR_UNSUPPORTED, "prefill_attention: head_dim=%d (only 128)", head_dim);
@@ -519,6 +532,7 @@ extern "C" int nsd_prefill_attention(const void* q, const void* k, const void* v
   args.o = static_cast<f16*>(o);
   args.lse = lse;
   args.cu_seqlens = cu_seqlens;
+  args.seq_order = seq_order;
   args.status = status;
   args.total_tokens = total_tokens;
   args.n_seqs = n_seqs;

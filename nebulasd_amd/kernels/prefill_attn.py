@@ -17,6 +17,24 @@ from .. import _lib
 from ._util import StatusWord, ptr, require, require_cuda, stream_of
 
 
+_ORDER_CACHE: dict = {}
+
+
+def _longest_first(cu_seqlens: torch.Tensor) -> torch.Tensor:
+    """Prompt indices, longest first (device int32, computed on the device with
+    no host synchronisation; cached per cu_seqlens tensor and version, so the
+    layers of one forward share it)."""
+    key = (cu_seqlens.data_ptr(), cu_seqlens._version, cu_seqlens.numel(), cu_seqlens.device)
+    order = _ORDER_CACHE.get(key)
+    if order is None:
+        lens = cu_seqlens[1:] - cu_seqlens[:-1]
+        order = torch.argsort(lens, descending=True, stable=True).to(torch.int32)
+        if len(_ORDER_CACHE) >= 16:
+            _ORDER_CACHE.clear()
+        _ORDER_CACHE[key] = order
+    return order
+
+
 def _launch(q, k, v, o, cu_seqlens, max_seqlen: int, softmax_scale: float,
             lse: torch.Tensor | None, validate: bool) -> None:
     require_cuda(q, k, v, o, cu_seqlens, lse)
@@ -36,8 +54,10 @@ def _launch(q, k, v, o, cu_seqlens, max_seqlen: int, softmax_scale: float,
         if lse.numel() != tokens * hq:
             raise ValueError("lse must be [tokens, Hq]")
     status = StatusWord(q.device) if validate else None
+    order = _longest_first(cu_seqlens)
     _lib.call("nsd_prefill_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-              ptr(lse), cu_seqlens.data_ptr(), cu_seqlens.numel() - 1, int(max_seqlen), tokens,
+              ptr(lse), cu_seqlens.data_ptr(), order.data_ptr(), cu_seqlens.numel() - 1,
+              int(max_seqlen), tokens,
               hq, hkv, d, float(softmax_scale), ptr(status.t) if status else None, stream_of(q))
     if status is not None:
         status.check("prefill_attention")

@@ -126,3 +126,34 @@ def test_prefill_repeatable(gpu):
     o1, l1 = run_prefill(w)
     o2, l2 = run_prefill(w)
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_prefill_prompt_order_is_only_a_schedule(gpu):
+    """The optional longest-first prompt order changes which workgroup runs
+    when, not the arithmetic: natural order, longest first and a reversed
+    order give bit-identical outputs; an entry outside the prompts is flagged."""
+    from nebulasd_amd import _lib
+
+    w = make_prefill_workload("prefill_target", 7, device=gpu, lens=[40, 700, 5, 300, 1000, 64])
+    mx = max(w.lens)
+    lens_t = w.cu_seqlens[1:] - w.cu_seqlens[:-1]
+    orders = [None, torch.argsort(lens_t, descending=True, stable=True).int(),
+              torch.arange(len(w.lens) - 1, -1, -1, dtype=torch.int32, device=gpu)]
+    outs = []
+    for order in orders:
+        o = torch.empty_like(w.q)
+        _lib.call("nsd_prefill_attention", w.q.data_ptr(), w.k.data_ptr(), w.v.data_ptr(), o.data_ptr(),
+                  None, w.cu_seqlens.data_ptr(), None if order is None else order.data_ptr(), len(w.lens),
+                  mx, w.tokens, w.q.shape[1], w.k.shape[1], 128, 128 ** -0.5, None,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(o)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    bad = torch.tensor([0, 1, 2, 3, 4, 6], dtype=torch.int32, device=gpu)  # 6 is past the prompts
+    o = torch.empty_like(w.q)
+    _lib.call("nsd_prefill_attention", w.q.data_ptr(), w.k.data_ptr(), w.v.data_ptr(), o.data_ptr(), None,
+              w.cu_seqlens.data_ptr(), bad.data_ptr(), len(w.lens), mx, w.tokens, w.q.shape[1],
+              w.k.shape[1], 128, 128 ** -0.5, status.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert status.item() & _lib.STATUS_BAD_SEQ
