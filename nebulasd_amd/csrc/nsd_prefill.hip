@@ -50,10 +50,10 @@ constexpr float kLazyMax = 8.f;
 
 // Kernel shape: NTW 16-row tiles per wave, NW waves per workgroup, KT tokens
 // per K/V tile, PF tiles of global loads in flight, LAZY running-max raise.
-template <int NTW_, int NW_, int KT_, int PF_, bool LAZY_, bool SP_ = false, int WPE_ = 1>
+template <int NTW_, int NW_, int KT_, int PF_, bool LAZY_, int WPE_ = 1>
 struct PrefillCfg {
   static constexpr int NTW = NTW_, NW = NW_, KT = KT_, PF = PF_;
-  static constexpr bool LAZY = LAZY_, SP = SP_;
+  static constexpr bool LAZY = LAZY_;
   static constexpr int WPE = WPE_;  // minimum waves per SIMD the register budget must allow
   static constexpr int rows = NW * 16 * NTW;  // query rows (position x q-head) per workgroup
   static constexpr int threads = NW * kWave;
@@ -68,8 +68,10 @@ struct PrefillCfg {
 // tiles, three workgroups per compute unit (168 VGPRs).  Measured against
 // 8-wave workgroups (one per CU), 64-token tiles, a second tile in flight,
 // 16- and 64-row waves and the software-pipelined loop, all slower; shapes
-// that spill registers were slowest.
-using PrefillShape = PrefillCfg<2, 4, 32, 1, true, false, 3>;
+// that spill registers were slowest, and so was a software-pipelined loop
+// (K one tile ahead of V, the next tile's score MFMAs issued beside the
+// softmax).
+using PrefillShape = PrefillCfg<2, 4, 32, 1, true, 3>;
 
 struct PrefillArgs {
   const f16* q;               // [T, Hq, D]
@@ -191,6 +193,7 @@ prefill_attn_kernel(PrefillArgs a) {
   for (int j = 0; j < NTW; ++j) {
     m[j] = -INFINITY;
     l[j] = 0.f;
+
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[j][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -289,173 +292,32 @@ prefill_attn_kernel(PrefillArgs a) {
     }
   };
 
-  if constexpr (C::SP) {
-    // Software pipeline: K runs one tile ahead of V.  While the softmax of
-    // tile t turns its scores into P, the wave issues the score MFMAs of tile
-    // t + 1 (K already in LDS) and the PV MFMAs of tile t, so the matrix
-    // cores and the VALU work at the same time.
-    constexpr int LPK = KT * (PD / 8) / NTHR;  // 16-byte loads per thread of one K or V tile
-    static_assert(LPK * NTHR == KT * (PD / 8), "K/V tile loads split evenly");
-    u32x4 kst[LPK], vst[LPK];
-    auto load_kv = [&](u32x4 (&st)[LPK], const f16* base, int t) {
-#pragma unroll
-      for (int i = 0; i < LPK; ++i) {
-        const int cc = threadIdx.x + i * NTHR;
-        const int tok = cc / (PD / 8), part = cc % (PD / 8);
-        const int tk = min(t * KT + tok, len - 1);  // past the prompt: masked, reads its last row
-        st[i] = *reinterpret_cast<const u32x4*>(base + ((int64_t)(start + tk) * a.hkv + kvh) * PD + part * 8);
-      }
-    };
-    auto store_kv = [&](const u32x4 (&st)[LPK], lds_char* dst) {
-#pragma unroll
-      for (int i = 0; i < LPK; ++i) {
-        const int cc = threadIdx.x + i * NTHR;
-        *(lds_u32x4*)(dst + (cc / (PD / 8)) * PROWB + (cc % (PD / 8)) * 16) = st[i];
-      }
-    };
-    lds_char* kbuf[2] = {s_kv, s_kv + KT * PROWB};
-    lds_char* vbuf[2] = {s_kv + 2 * KT * PROWB, s_kv + 3 * KT * PROWB};
-    auto score = [&](const lds_char* kb, f32x4 (&sc)[KH][NTW]) {
-#pragma unroll
-      for (int h = 0; h < KH; ++h)
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) sc[h][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-        for (int h = 0; h < KH; ++h) {
-          const f16x8 kf = *(const lds_f16x8*)(kb + (16 * h + lr) * PROWB + 64 * kk + 16 * lg);
-#pragma unroll
-          for (int j = 0; j < NTW; ++j) sc[h][j] = mfma_k32(kf, qf[j][kk], sc[h][j]);
-        }
-      }
-    };
-    // Softmax of tile t's scores `sc` and its PV product from `vb`; the score
-    // MFMAs of the next tile (`kb_next` into `sn`) are issued in the same
-    // basic block.
-    auto step = [&](int t, f32x4 (&sc)[KH][NTW], const lds_char* vb, const lds_char* kb_next,
-                    f32x4 (&sn)[KH][NTW]) {
-      const int t0 = t * KT;
-      if (t0 + KT - 1 >= p0) {  // causal mask (also hides tokens past the prompt)
-#pragma unroll
-        for (int h = 0; h < KH; ++h)
-#pragma unroll
-          for (int j = 0; j < NTW; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (t0 + 16 * h + 4 * lg + i > pos_row[j]) sc[h][j][i] = -INFINITY;
-      }
-      float mxs[NTW];
-      bool raise = false;
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int h = 0; h < KH; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[h][j][i]);
-        mxs[j] = mx * c;
-        raise |= mxs[j] > m[j] + kLazyMax;
-      }
-      if (__any(raise)) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 16, kWave));
-          mxs[j] = fmaxf(mxs[j], __shfl_xor(mxs[j], 32, kWave));
-          const float m_new = fmaxf(m[j], mxs[j]);
-          const float alpha = __builtin_amdgcn_exp2f(m[j] - (m_new == -INFINITY ? 0.f : m_new));
-          l[j] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
-          m[j] = m_new;
-        }
-      }
-      score(kb_next, sn);
-      f16x8 pf[KT / 32][NTW];
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const float m_use = m[j] == -INFINITY ? 0.f : m[j];
-        float ps = 0.f;
-#pragma unroll
-        for (int h = 0; h < KH; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[h][j][i], c, -m_use));
-            ps += pv;
-            pf[h / 2][j][4 * (h % 2) + i] = (f16)pv;
-          }
-        l[j] += ps;
-      }
-#pragma unroll
-      for (int ks = 0; ks < KT / 32; ++ks) {
-        const lds_char* vsrc = vb + (32 * ks + 4 * lg + (lr >> 2)) * PROWB + 8 * (lr & 3);
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const f16x4 lo = ds_read_tr16(vsrc + 32 * dt);
-          const f16x4 hi = ds_read_tr16(vsrc + 16 * PROWB + 32 * dt);
-          const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-          for (int j = 0; j < NTW; ++j) acc[j][dt] = mfma_k32(vf, pf[ks][j], acc[j][dt]);
-        }
-      }
-    };
-
-    // Prologue: K(0), V(0), K(1) staged; scores of tile 0.
-    load_kv(kst, a.k, 0);
-    load_kv(vst, a.v, 0);
-    store_kv(kst, kbuf[0]);
-    store_kv(vst, vbuf[0]);
-    if (n_tiles > 1) {
-      load_kv(kst, a.k, 1);
-      store_kv(kst, kbuf[1]);
-    }
-    __syncthreads();
-    f32x4 sa[KH][NTW], sb[KH][NTW];
-    score(kbuf[0], sa);
-    __syncthreads();  // every wave has read K(0) before K(2) replaces it
-    // Iteration t: loads of K(t+2), V(t+1); step(t); stores; one barrier.
-    auto iteration = [&](auto par, int t, f32x4 (&sc)[KH][NTW], f32x4 (&sn)[KH][NTW]) {
-      constexpr int B = decltype(par)::value;  // t % 2
-      if (t + 2 < n_tiles) load_kv(kst, a.k, t + 2);
-      if (t + 1 < n_tiles) load_kv(vst, a.v, t + 1);
-      step(t, sc, vbuf[B], kbuf[B ^ 1], sn);  // past the last tile the next scores are unused
-      if (t + 2 < n_tiles) store_kv(kst, kbuf[B]);
-      if (t + 1 < n_tiles) store_kv(vst, vbuf[B ^ 1]);
-      __syncthreads();
-    };
-    for (int t = 0; t < n_tiles; t += 2) {
-      iteration(std::integral_constant<int, 0>{}, t, sa, sb);
-      if (t + 1 < n_tiles) iteration(std::integral_constant<int, 1>{}, t + 1, sb, sa);
-    }
-  } else {
   // Pipeline: tile t is computed from LDS buffer t % 2 while the loads of
-    // tile t + PF are in flight; tile t + 1 (loaded PF - 1 tiles earlier) goes
-    // to the other buffer after the compute, then one barrier.
-    using std::integral_constant;
-    load_tile(integral_constant<int, 0>{}, 0);
-    if constexpr (C::PF == 2) {
-      if (n_tiles > 1) load_tile(integral_constant<int, 1>{}, 1);
+  // tile t + PF are in flight; tile t + 1 (loaded PF - 1 tiles earlier) goes
+  // to the other buffer after the compute, then one barrier.
+  using std::integral_constant;
+  load_tile(integral_constant<int, 0>{}, 0);
+  if constexpr (C::PF == 2) {
+    if (n_tiles > 1) load_tile(integral_constant<int, 1>{}, 1);
+  }
+  store_tile(integral_constant<int, 0>{}, 0);
+  __syncthreads();
+  auto iteration = [&](auto par, int t) {
+    constexpr int S = decltype(par)::value;  // t % 2
+    if constexpr (C::PF == 1) {
+      if (t + 1 < n_tiles) load_tile(integral_constant<int, 0>{}, t + 1);
+      compute(t, S);
+      if (t + 1 < n_tiles) store_tile(integral_constant<int, 0>{}, S ^ 1);
+    } else {
+      if (t + 2 < n_tiles) load_tile(integral_constant<int, S>{}, t + 2);
+      compute(t, S);
+      if (t + 1 < n_tiles) store_tile(integral_constant<int, S ^ 1>{}, S ^ 1);
     }
-    store_tile(integral_constant<int, 0>{}, 0);
     __syncthreads();
-    auto iteration = [&](auto par, int t) {
-      constexpr int S = decltype(par)::value;  // t % 2
-      if constexpr (C::PF == 1) {
-        if (t + 1 < n_tiles) load_tile(integral_constant<int, 0>{}, t + 1);
-        compute(t, S);
-        if (t + 1 < n_tiles) store_tile(integral_constant<int, 0>{}, S ^ 1);
-      } else {
-        if (t + 2 < n_tiles) load_tile(integral_constant<int, S>{}, t + 2);
-        compute(t, S);
-        if (t + 1 < n_tiles) store_tile(integral_constant<int, S ^ 1>{}, S ^ 1);
-      }
-      __syncthreads();
-    };
-    for (int t = 0; t < n_tiles; t += 2) {
-      iteration(integral_constant<int, 0>{}, t);
-      if (t + 1 < n_tiles) iteration(integral_constant<int, 1>{}, t + 1);
-    }
-
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    iteration(integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) iteration(integral_constant<int, 1>{}, t + 1);
   }
 
   // Normalise and write the valid rows.
