@@ -206,6 +206,61 @@ int nsd_prefill_attention(const void* q, const void* k, const void* v, void* o, 
                           int64_t total_tokens, int num_q_heads, int num_kv_heads, int head_dim,
                           float softmax_scale, int32_t* status, void* stream);
 
+/*
+ * Block-table metadata (the writes that produce the attention path's index
+ * input).  block_table: device int32 [bt_rows, bt_stride]; num_alloc: device
+ * int32 [bt_rows] (swiftLLM's num_seq_allocated_blocks); is_block_free:
+ * device bool/uint8 [num_blocks].  Out-of-range rows, counts or block ids
+ * are skipped and flagged in *status (NSD_STATUS_BAD_SEQ / _BAD_BLOCK).
+ *
+ * nsd_write_block_ranges: row rows[i] gets begins[i] + 0..counts[i]-1 in its
+ * first counts[i] entries (and num_alloc[rows[i]] = counts[i] when num_alloc
+ * is not NULL).  Replaces the bank metadata writer of
+ * nebulasd/src/nebulasd/workers/dma_process.py:95-125 (host index/value
+ * arrays, two H2D copies, index_copy_) and the per-request fill of
+ * swiftLLM/swiftllm/worker/block_manager.py:685-691.  rows/begins/counts:
+ * device int32 [n_ranges].
+ */
+int nsd_write_block_ranges(int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
+                           const int32_t* rows, const int32_t* begins, const int32_t* counts,
+                           int64_t n_ranges, int32_t* num_alloc, int32_t* status, void* stream);
+
+/*
+ * set_block_table_and_num_seq_alloc_blocks
+ * (swiftLLM/swiftllm/worker/kernels/block_mgmt.py:5-45): for batch entry i
+ * with seq s, block_table[s][num_alloc[s] + j] = candidate_blocks[c_i + j]
+ * for j < block_needed[i], where c_i is the sum of block_needed[0..i-1];
+ * then num_alloc[s] += block_needed[i].  seq_ids must be distinct (as in the
+ * reference, whose programs would race otherwise).
+ */
+int nsd_set_block_table(int32_t* num_alloc, int32_t* block_table, int64_t bt_rows,
+                        int64_t bt_stride, const int32_t* candidate_blocks, int64_t n_candidates,
+                        const int32_t* seq_ids, const int32_t* block_needed, int64_t batch,
+                        int32_t* status, void* stream);
+
+/*
+ * unset_block_table_and_num_seq_alloc_blocks (block_mgmt.py:48-80): marks
+ * block_table[s][0 .. num_alloc[s]) free in is_block_free and sets
+ * num_alloc[s] = 0 for every s in seq_ids.
+ */
+int nsd_unset_block_table(int32_t* num_alloc, const int32_t* block_table, int64_t bt_rows,
+                          int64_t bt_stride, const int32_t* seq_ids, int64_t batch,
+                          uint8_t* is_block_free, int64_t num_blocks, int32_t* status,
+                          void* stream);
+
+/*
+ * gather_allocated_blocks_and_unset (block_mgmt.py:83-127): as
+ * nsd_unset_block_table, and the freed ids of seq_ids[0], seq_ids[1], ... are
+ * written back to back into `gathered` (capacity entries; the reference
+ * sizes it with the sum of num_alloc[seq_ids]).  batch <= 4096.
+ */
+int nsd_gather_allocated_blocks_and_unset(int32_t* num_alloc, const int32_t* block_table,
+                                          int64_t bt_rows, int64_t bt_stride,
+                                          const int32_t* seq_ids, int64_t batch,
+                                          uint8_t* is_block_free, int64_t num_blocks,
+                                          int32_t* gathered, int64_t gathered_capacity,
+                                          int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

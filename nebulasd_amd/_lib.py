@@ -55,6 +55,18 @@ SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
                 c_int, c_int, c_int, c_void_p, c_int64, _I32P, c_void_p, c_void_p, c_int64,
                 c_float, c_void_p, c_void_p]),
+    "nsd_write_block_ranges": (
+        c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                c_void_p]),
+    "nsd_set_block_table": (
+        c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                c_void_p, c_void_p]),
+    "nsd_unset_block_table": (
+        c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                c_void_p]),
+    "nsd_gather_allocated_blocks_and_unset": (
+        c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                c_int64, c_void_p, c_void_p]),
     "nsd_prefill_attention": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                 c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),

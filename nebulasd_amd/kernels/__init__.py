@@ -1,5 +1,7 @@
 """gfx950 kernels behind swiftLLM's kernel entry points (swiftllm.worker.kernels)."""
 
+from .block_mgmt import (gather_allocated_blocks_and_unset, set_block_table_and_num_seq_alloc_blocks,
+                         unset_block_table_and_num_seq_alloc_blocks, write_block_table_ranges)
 from .kvcache_mgmt import store_kvcache
 from .paged_attn import paged_attention
 from .prefill_attn import flash_attn_varlen_func, prefill_attention
@@ -8,4 +10,6 @@ from .rmsnorm import rmsnorm_inplace
 from .rotary_emb import rotary_embedding_inplace
 
 __all__ = ["paged_attention", "store_kvcache", "rotary_embedding_inplace", "rmsnorm_inplace",
-           "qk_norm_rope_store", "flash_attn_varlen_func", "prefill_attention"]
+           "qk_norm_rope_store", "flash_attn_varlen_func", "prefill_attention",
+           "set_block_table_and_num_seq_alloc_blocks", "unset_block_table_and_num_seq_alloc_blocks",
+           "gather_allocated_blocks_and_unset", "write_block_table_ranges"]
