@@ -46,6 +46,7 @@ def parse_args():
                    help="comma-separated workloads measured beside the headline ('' to skip)")
     p.add_argument("--prefill", default="prefill_target,prefill_draft",
                    help="comma-separated prefill-attention workloads ('' to skip)")
+    p.add_argument("--block-table", type=int, default=1, help="1: time the block-table metadata writer")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -275,6 +276,70 @@ def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: 
     return res
 
 
+def measure_block_table(seed: int, reps: int = 50):
+    """Bank-switch metadata: 128 block-table rows get contiguous ranges of
+    U[0, 256] blocks.  Host-to-completion latency per write (median over
+    `reps`, synchronised) of this build's writer and of the reference's
+    formulation (dma_process.py:111-121: host index/value arrays in pinned
+    memory, two H2D copies, index_copy_, event sync)."""
+    import numpy as np
+    import torch
+
+    from nebulasd_amd.kernels import write_block_table_ranges
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+    rows_n, stride = 128, 2560
+    rows = rng.permutation(rows_n).tolist()
+    counts = rng.integers(0, 257, rows_n).tolist()
+    begins = np.cumsum([0] + counts[:-1]).tolist()
+    bt = torch.zeros((rows_n, stride), dtype=torch.int32, device=dev)
+    na = torch.zeros(rows_n, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream()
+    cap = sum(counts)
+    indices = torch.empty(cap, dtype=torch.int64, pin_memory=True)
+    values = torch.empty(cap, dtype=torch.int32, pin_memory=True)
+    gi, gv = torch.empty_like(indices, device=dev), torch.empty_like(values, device=dev)
+    ix, val = indices.numpy(), values.numpy()
+
+    def ours():
+        with torch.cuda.stream(stream):
+            write_block_table_ranges(bt, rows, begins, counts, na)
+        stream.synchronize()
+
+    def reference():
+        n = 0
+        for row, begin, count in zip(rows, begins, counts):
+            ix[n:n + count] = np.arange(row * stride, row * stride + count)
+            val[n:n + count] = np.arange(begin, begin + count)
+            n += count
+        with torch.cuda.stream(stream):
+            gi[:n].copy_(indices[:n], non_blocking=True)
+            gv[:n].copy_(values[:n], non_blocking=True)
+            bt.view(-1).index_copy_(0, gi[:n], gv[:n])
+            done = torch.cuda.Event()
+            done.record(stream)
+        done.synchronize()
+
+    out = {}
+    for name, fn in (("ours", ours), ("reference", reference)):
+        for _ in range(5):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e6)
+        out[name] = float(np.median(ts))
+    ref_bt = bt.clone()
+    ours()
+    same = bool(torch.equal(bt, ref_bt))
+    return {"workload": "block_table_bank_switch", "kind": "metadata", "rows": rows_n,
+            "blocks_written": cap, "us_per_write": out["ours"], "reference_us_per_write": out["reference"],
+            "speedup_vs_reference": out["reference"] / out["ours"], "identical_tables": same,
+            "note": "host-to-completion latency, median of %d synchronised writes" % reps}
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch for `workload`, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy
@@ -401,6 +466,11 @@ def main():
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, {r2['tflops']:.0f} TFLOP/s "
               f"(reference SDPA loop {r2['reference_sdpa_loop_us']:.0f} us)", file=sys.stderr, flush=True)
         secondary[name] = r2
+    if args.block_table:
+        r2 = measure_block_table(args.seed)
+        print(f"# block table bank switch: {r2['us_per_write']:.1f} us per write "
+              f"(reference formulation {r2['reference_us_per_write']:.1f} us)", file=sys.stderr, flush=True)
+        secondary[r2["workload"]] = r2
     for name in filter(None, args.secondary.split(",")):
         r2, w2 = measure(name, args.seed, args.steps, args.warmup)
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
