@@ -47,6 +47,7 @@ def parse_args():
     p.add_argument("--prefill", default="prefill_target,prefill_draft",
                    help="comma-separated prefill-attention workloads ('' to skip)")
     p.add_argument("--block-table", type=int, default=1, help="1: time the block-table metadata writer")
+    p.add_argument("--hostkv", type=int, default=1, help="1: time the HostKV block-range copies")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -340,6 +341,171 @@ def measure_block_table(seed: int, reps: int = 50):
             "note": "host-to-completion latency, median of %d synchronised writes" % reps}
 
 
+HOST_LINK_PEAK_GBPS = 64.0  # PCIe 5.0 x16, one direction: 32 GT/s x 16 lanes / 8
+
+
+def _hip_runtime():
+    """The HIP runtime the native library is bound to (ctypes handle), for
+    the reference's own call pattern: hipMemcpyAsync through ctypes."""
+    import ctypes
+
+    from nebulasd_amd import _lib
+
+    _lib.load()
+    with open("/proc/self/maps") as f:
+        paths = {line.split()[-1] for line in f if "libamdhip64" in line}
+    hip = ctypes.CDLL(sorted(paths)[0])
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                   ctypes.c_void_p]
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    return hip
+
+
+def measure_hostkv(seed: int, reps: int = 6):
+    """HostKV copies of Qwen3-8B blocks (1,179,648 bytes per K or V block) in
+    the layout of the reference's copy benchmark
+    (nebulasd/tests/support/copy_benchmark.py:11-56): 8 requests of 32
+    blocks, a guard block each side, one region per request, D2H then H2D;
+    then a swap of 128 scattered single blocks each way.  Copy interval from
+    events on the copy stream, median of `reps`.  Legs: the reference's
+    formulation (one hipMemcpyAsync per region and plane through ctypes,
+    cuda_transfer.py:93-106 with cuda_memcpy.py:52-55), the DMA engine and
+    the kernel engine.  Bytes are compared after the timed copies."""
+    import numpy as np
+    import torch
+
+    from nebulasd_amd.hostkv import HostKVArena, copy_block_ranges, swap_blocks
+
+    dev = torch.device("cuda:0")
+    shape = (36, 8, 16, 128)
+    batch, blocks = 8, 32
+    cap = blocks + 2
+    nb = batch * cap
+    k = torch.empty((nb, *shape), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    bb = k[0].numel() * 2
+    arena = HostKVArena.create(total_blocks=nb, block_bytes=bb, kv_block_shape=shape)
+    addr, plane = arena.address(), arena.descriptor.plane_bytes
+    hip = _hip_runtime()
+    stream = torch.cuda.Stream()
+    regions = [(i * cap + 1, i * cap + 1, blocks) for i in range(batch)]
+    g_, h_, c_ = zip(*regions)
+    plan_bytes = 2 * batch * blocks * bb
+
+    scratch = torch.empty_like(k)
+
+    def randomize():
+        """Fresh random bytes on both sides (the host planes through a pinned
+        copy of a random device buffer, so every block differs)."""
+        for host in (arena.k, arena.v):
+            scratch.view(torch.int16).random_(-30000, 30000)
+            host.view(-1).copy_(scratch.view(torch.uint8).view(-1))
+        k.view(torch.int16).random_(-30000, 30000)
+        v.view(torch.int16).random_(-30000, 30000)
+        torch.cuda.synchronize()
+
+    def reference(direction):
+        kind = 2 if direction == "D2H" else 1
+        for g, h, c in regions:
+            n = c * bb
+            for cache, host in ((k, addr), (v, addr + plane)):
+                gpu_p, host_p = cache.data_ptr() + g * bb, host + h * bb
+                dst, src = (host_p, gpu_p) if direction == "D2H" else (gpu_p, host_p)
+                rc = hip.hipMemcpyAsync(dst, src, n, kind, stream.cuda_stream)
+                if rc:
+                    raise RuntimeError(f"hipMemcpyAsync failed with status {rc}")
+
+    def engine(name):
+        return lambda direction: copy_block_ranges(k, v, addr, addr + plane, nb, g_, h_, c_, direction, name,
+                                                   stream.cuda_stream)
+
+    def timed_once(fn, *a):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        fn(*a)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e6
+
+    def same_bytes():
+        ok = True
+        for g, h, c in regions:
+            for cache, host in ((k, arena.k), (v, arena.v)):
+                ok &= bool(torch.equal(cache[g:g + c].view(torch.uint8).reshape(c, -1).cpu(), host[h:h + c]))
+        return ok
+
+    legs = (("reference", reference), ("dma", engine("dma")), ("kernel", engine("kernel")))
+    out, identical = {}, True
+    for direction in ("D2H", "H2D"):
+        # untimed pass per leg: fresh bytes on both sides, copy, compare
+        for _, fn in legs:
+            randomize()
+            fn(direction)
+            stream.synchronize()
+            identical &= same_bytes()
+        # timed rounds, leg order alternating (as copy_benchmark.py:31 alternates its paths)
+        for _, fn in legs:
+            fn(direction)
+        stream.synchronize()
+        samples = {leg: ([], []) for leg, _ in legs}
+        for rnd in range(reps):
+            for leg, fn in (legs if rnd % 2 == 0 else legs[::-1]):
+                ms, us = timed_once(fn, direction)
+                samples[leg][0].append(plan_bytes / ms / 1e6)
+                samples[leg][1].append(us)
+        row = {}
+        for leg, (gbps, us) in samples.items():
+            row[f"{leg}_gbps"] = float(np.median(gbps))
+            row[f"{leg}_gbps_min_max"] = [float(min(gbps)), float(max(gbps))]
+            row[f"{leg}_host_to_completion_us"] = float(np.median(us))
+        out[direction] = row
+
+    def timed(fn, *a):
+        fn(*a)
+        stream.synchronize()
+        return float(np.median([timed_once(fn, *a)[0] for _ in range(reps)])), None
+
+    # swap_blocks: 128 scattered single blocks (runs of consecutive ids are rare)
+    rng = np.random.default_rng(seed)
+    gpu_ids = rng.permutation(nb)[:128].tolist()
+    host_ids = rng.permutation(nb)[:128].tolist()
+    ks, vs = arena.k.view(nb, *shape[:-1], 2 * shape[-1]), arena.v.view(nb, *shape[:-1], 2 * shape[-1])
+    ks, vs = ks.view(torch.float16), vs.view(torch.float16)
+    swap = {}
+    for is_in in (False, True):
+        src, dst = (host_ids, gpu_ids) if is_in else (gpu_ids, host_ids)
+        row = {}
+        for name in ("dma", "kernel"):
+            def fn(name=name):
+                with torch.cuda.stream(stream):
+                    swap_blocks(src, dst, is_in, k, v, ks, vs, engine=name)
+            randomize()
+            ms, _ = timed(fn)
+            for gi, hi in zip(gpu_ids, host_ids):
+                identical &= bool(torch.equal(k[gi].view(torch.uint8).reshape(-1).cpu(), arena.k[hi]))
+            row[f"{name}_gbps"] = 2 * 128 * bb / ms / 1e6
+        swap["in" if is_in else "out"] = row
+    # the link's ceiling as torch's own pinned copy of one whole plane sees it
+    flat_dev, flat_host = k.view(torch.uint8).view(-1), arena.k.view(-1)
+    ceil = {}
+    for d, fn in (("H2D", lambda: flat_dev.copy_(flat_host, non_blocking=True)),
+                  ("D2H", lambda: flat_host.copy_(flat_dev, non_blocking=True))):
+        with torch.cuda.stream(stream):
+            ms, _ = timed(fn)
+        ceil[d] = plane / ms / 1e6
+    best = min(max(out[d]["dma_gbps"], out[d]["kernel_gbps"]) for d in out)
+    return {"workload": "hostkv_copy", "kind": "host_link", "block_bytes": bb, "requests": batch,
+            "blocks_per_request": blocks, "bytes_per_plan": plan_bytes, **out,
+            "swap_128_scattered_blocks": swap, "torch_pinned_copy_gbps": ceil,
+            "roofline": {"bound": "host_link", "achieved": best, "peak": HOST_LINK_PEAK_GBPS, "unit": "GB/s",
+                         "frac": best / HOST_LINK_PEAK_GBPS},
+            "identical_bytes": identical,
+            "note": ("copy interval from events on the copy stream; median (and min, max) of %d plans per leg, "
+                     "legs in alternating order; bytes compared in a separate untimed pass per leg" % reps)}
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch for `workload`, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy
@@ -470,6 +636,14 @@ def main():
         r2 = measure_block_table(args.seed)
         print(f"# block table bank switch: {r2['us_per_write']:.1f} us per write "
               f"(reference formulation {r2['reference_us_per_write']:.1f} us)", file=sys.stderr, flush=True)
+        secondary[r2["workload"]] = r2
+    if args.hostkv:
+        r2 = measure_hostkv(args.seed)
+        print("# hostkv copy (GB/s, reference / dma / kernel): " + "; ".join(
+            f"{d} {r2[d]['reference_gbps']:.1f} / {r2[d]['dma_gbps']:.1f} / {r2[d]['kernel_gbps']:.1f}"
+            for d in ("D2H", "H2D")) + "; scattered swap-in dma / kernel: "
+            f"{r2['swap_128_scattered_blocks']['in']['dma_gbps']:.1f} / "
+            f"{r2['swap_128_scattered_blocks']['in']['kernel_gbps']:.1f}", file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     for name in filter(None, args.secondary.split(",")):
         r2, w2 = measure(name, args.seed, args.steps, args.warmup)

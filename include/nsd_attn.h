@@ -40,6 +40,11 @@ extern "C" {
 #define NSD_STATUS_BAD_SEQ 2       /* seq_id outside [0, bt_rows) or position outside the row */
 #define NSD_STATUS_BAD_POSITION 4  /* RoPE position outside the cos/sin table */
 
+#define NSD_COPY_D2H 0            /* device cache -> host plane (write-back / swap-out) */
+#define NSD_COPY_H2D 1            /* host plane -> device cache (restore / swap-in) */
+#define NSD_COPY_ENGINE_DMA 0     /* hipMemcpyAsync per run (system DMA engines) */
+#define NSD_COPY_ENGINE_KERNEL 1  /* one gfx950 copy launch over every run */
+
 #define NSD_PLAN_HEADER_WORDS 20
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -260,6 +265,45 @@ int nsd_gather_allocated_blocks_and_unset(int32_t* num_alloc, const int32_t* blo
                                           uint8_t* is_block_free, int64_t num_blocks,
                                           int32_t* gathered, int64_t gathered_capacity,
                                           int32_t* status, void* stream);
+
+/*
+ * HostKV block-range copies: byte images of KV-cache blocks between the
+ * device caches k_cache/v_cache (gpu_blocks blocks of block_bytes each,
+ * block-major) and two host planes host_k/host_v (host_blocks blocks each).
+ *
+ * nsd_copy_block_ranges: one copy plan of the HostKV DMA backend
+ * (nebulasd/src/nebulasd/kv/cuda_transfer.py:78-108).  Region i moves
+ * block_count[i] blocks starting at device block gpu_begin_block[i] and
+ * host block host_begin_block[i] (the reference's
+ * extent.offset_blocks + host_begin_block), K plane and V plane, in
+ * `direction`.  Region arrays are HOST int64 [n_regions].  Every range is
+ * checked before anything is enqueued ("copy exceeds GPU KV cache",
+ * "copy exceeds HostKV plane", "negative copy range": NSD_ERR_INVALID).
+ * Zero-count regions are skipped; regions that continue the previous one on
+ * both sides merge into one run.  engine NSD_COPY_ENGINE_DMA keeps the
+ * plan's order (a later region wins where destinations overlap);
+ * NSD_COPY_ENGINE_KERNEL needs pinned host planes, 16-byte alignment and
+ * disjoint destinations (NSD_ERR_INVALID / NSD_ERR_UNSUPPORTED otherwise).
+ * Asynchronous on `stream`; the host planes must stay alive until it ends.
+ */
+int nsd_copy_block_ranges(void* k_cache, void* v_cache, int64_t gpu_blocks, void* host_k,
+                          void* host_v, int64_t host_blocks, int64_t block_bytes,
+                          const int64_t* gpu_begin_block, const int64_t* host_begin_block,
+                          const int64_t* block_count, int64_t n_regions, int direction,
+                          int engine, void* stream);
+
+/*
+ * nsd_swap_blocks: swiftLLM's swap_blocks (swiftLLM/csrc/src/block_swapping.cpp:22-85).
+ * source_block_ids[i] is copied to target_block_ids[i] (HOST int64 [n]);
+ * is_swap_in != 0 copies swap space -> device cache, else device cache ->
+ * swap space; K and V both.  Runs of consecutive ids on both sides are one
+ * copy, as in the reference.  Ids are range-checked (the reference does
+ * not check them); engines as for nsd_copy_block_ranges.
+ */
+int nsd_swap_blocks(const int64_t* source_block_ids, const int64_t* target_block_ids, int64_t n,
+                    int is_swap_in, void* k_cache, void* v_cache, int64_t gpu_blocks,
+                    void* k_swap, void* v_swap, int64_t swap_blocks, int64_t block_bytes,
+                    int engine, void* stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,10 @@ STATUS_BAD_BLOCK = 1
 STATUS_BAD_SEQ = 2
 STATUS_BAD_POSITION = 4
 PLAN_HEADER_WORDS = 20
+COPY_D2H = 0
+COPY_H2D = 1
+COPY_ENGINE_DMA = 0
+COPY_ENGINE_KERNEL = 1
 
 # Plan header word indices (nsd_common.h, enum PlanHeader).
 PLAN_MAGIC, PLAN_VERSION, PLAN_ROWS, PLAN_GROUPS, PLAN_PIECES, PLAN_WORKERS, PLAN_COMBINES, \
@@ -67,6 +71,12 @@ SIGNATURES = {
     "nsd_gather_allocated_blocks_and_unset": (
         c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                 c_int64, c_void_p, c_void_p]),
+    "nsd_copy_block_ranges": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+                c_void_p, c_int64, c_int, c_int, c_void_p]),
+    "nsd_swap_blocks": (
+        c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                c_int64, c_int64, c_int, c_void_p]),
     "nsd_prefill_attention": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                 c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),
