@@ -305,6 +305,52 @@ int nsd_swap_blocks(const int64_t* source_block_ids, const int64_t* target_block
                     void* k_swap, void* v_swap, int64_t swap_blocks, int64_t block_bytes,
                     int engine, void* stream);
 
+/*
+ * The rest of the layer around the attention path (swiftLLM's element-wise
+ * kernels between the GEMMs, and the post-layer argmax).  fp16 data, fp32
+ * arithmetic, in place where the reference is in place.
+ *
+ * nsd_fused_add_rmsnorm_inplace: fused_add_rmsnorm_inplace
+ * (swiftLLM/swiftllm/worker/kernels/rmsnorm.py:74-89, kernel :39-72): per row,
+ * residual = x + residual (one fp16 rounding), then
+ * x = fp16(residual * 1/sqrt(mean(residual^2) + eps) * weight) in fp32.
+ * hidden a multiple of 8 and <= 8192; pointers 16-byte aligned.
+ */
+int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void* weight, int64_t n_rows,
+                                  int64_t hidden, float eps, void* stream);
+
+/*
+ * nsd_silu_and_mul_inplace: silu_and_mul_inplace
+ * (swiftLLM/swiftllm/worker/kernels/silu_and_mul.py:25-34, kernel :5-23): x is
+ * [n_tokens, 2 * inter_dim]; x[t, j] = x[t, j] * fp16(g / (1 + exp(-g))) with
+ * g = x[t, inter_dim + j] in fp32, for j < inter_dim (the product rounded once
+ * to fp16).  inter_dim a multiple of 8; x 16-byte aligned.
+ */
+int nsd_silu_and_mul_inplace(void* x, int64_t n_tokens, int64_t inter_dim, void* stream);
+
+/*
+ * nsd_lm_head_argmax: the post-layer's logits and argmax
+ * (swiftLLM/swiftllm/worker/layers/post_layer.py:70-71,
+ * `argmax(linear(last_input, lm_head), dim=1)`) without the logits tensor:
+ * tokens[r] = the first v maximising fp16(sum_h x[r][h] * lm_head[v][h])
+ * (fp32 sums; a NaN logit counts as the maximum, -0 equals +0, as in
+ * torch.argmax).  x [n_rows, hidden] and lm_head [vocab, hidden] fp16
+ * row-major; hidden a multiple of 128.  keys: device uint64 [n_rows] that
+ * must be zero on entry; the call leaves it zero.  tokens: device int64
+ * [n_rows].  Calls that share `keys` must not overlap.  Rows are processed
+ * in passes of 128 (each pass reads lm_head once).
+ */
+int nsd_lm_head_argmax(const void* x, const void* lm_head, int64_t n_rows, int64_t hidden,
+                       int64_t vocab, uint64_t* keys, int64_t* tokens, void* stream);
+
+/*
+ * nsd_argmax_rows: torch.argmax(logits, dim=1) over fp16 logits
+ * [n_rows, vocab] (first maximum; NaN counts as the maximum) into int64
+ * tokens [n_rows] (post_layer.py:71 when the logits are materialised).
+ */
+int nsd_argmax_rows(const void* logits, int64_t n_rows, int64_t vocab, int64_t* tokens,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

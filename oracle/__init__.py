@@ -10,9 +10,10 @@ product path (``nebulasd_amd``) never imports it and has no CPU fallback.
 Every function cites the reference file:line it follows.  How each function
 is pinned (closed forms, invariants, library routines, the reference's own
 literal test cases) is listed in the headers of ``oracle/attention.py`` and
-``oracle/blocks.py`` and ``oracle/hostkv.py``.
+``oracle/blocks.py``, ``oracle/hostkv.py`` and ``oracle/layer.py``.
 """
 
 from .attention import *  # noqa: F401,F403
 from .blocks import *  # noqa: F401,F403
 from .hostkv import *  # noqa: F401,F403
+from .layer import *  # noqa: F401,F403

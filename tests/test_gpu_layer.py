@@ -1,0 +1,175 @@
+"""GPU parity of the rest-of-layer kernels (fused add-RMSNorm, SiLU-and-mul,
+lm_head + argmax, argmax) against the numpy oracle, and against the
+reference's own torch formulation on the same GPU.
+
+Every case prints its name first (pytest -v) so a failing GPU step is named.
+Tolerances: residual and argmax over given logits bit-exact; normalised and
+activated values within 1e-3 (fp16 output, one rounding apart); lm_head
+argmax equal to the float64 reference's except where the two candidates'
+float64 logits are within 2e-3 of each other (accumulation order decides a
+near tie).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from nebulasd_amd import _lib
+from nebulasd_amd.kernels import fused_add_rmsnorm_inplace, silu_and_mul_inplace
+from nebulasd_amd.kernels.post_layer import (argmax_rows, last_token_indices, lm_head_argmax,
+                                             post_layer_forward)
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(gpu, *shape, scale=1.0, seed=0):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    return (torch.randn(shape, device=gpu, generator=g) * scale).half()
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (80, 4096), (4097, 1024), (33, 8), (7, 2056), (5, 8192)])
+def test_fused_add_rmsnorm_matches_oracle(gpu, rows, hidden):
+    x, r = _randn(gpu, rows, hidden, seed=1), _randn(gpu, rows, hidden, seed=2, scale=4.0)
+    w = (torch.rand(hidden, device=gpu) + 0.5).half()
+    want_x, want_r = oracle.fused_add_rmsnorm(x.cpu().numpy(), r.cpu().numpy(), w.cpu().numpy(), 1e-6)
+    fused_add_rmsnorm_inplace(x, r, w, 1e-6)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.cpu().numpy(), want_r)
+    got = x.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, want_x.astype(np.float64), rtol=1e-3, atol=1e-5)
+    print(f"fused_add_rmsnorm {rows}x{hidden}: exact {np.mean(got == want_x.astype(np.float64)):.4f}", flush=True)
+
+
+def test_fused_add_rmsnorm_rejects_bad_shapes(gpu):
+    x = torch.zeros(2, 8200, dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.NativeLibraryError, match="hidden=8200"):
+        fused_add_rmsnorm_inplace(x, x.clone(), torch.ones(8200, dtype=torch.float16, device=gpu), 1e-6)
+    x = torch.zeros(2, 12, dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.NativeLibraryError, match="hidden=12"):
+        fused_add_rmsnorm_inplace(x, x.clone(), torch.ones(12, dtype=torch.float16, device=gpu), 1e-6)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 12288), (80, 12288), (3000, 3072), (5, 8)])
+def test_silu_and_mul_matches_oracle(gpu, rows, inter):
+    x = _randn(gpu, rows, 2 * inter, scale=3.0, seed=3)
+    x0 = x.cpu().numpy()
+    want = oracle.silu_and_mul(x0)
+    silu_and_mul_inplace(x)
+    torch.cuda.synchronize()
+    got = x.cpu().numpy()
+    np.testing.assert_array_equal(got[:, inter:], x0[:, inter:])  # the gate half is left alone
+    np.testing.assert_allclose(got[:, :inter].astype(np.float64), want.astype(np.float64), rtol=2e-3, atol=1e-6)
+    exact = np.mean(got[:, :inter] == want)
+    assert exact > 0.99
+    print(f"silu_and_mul {rows}x{inter}: exact {exact:.4f}", flush=True)
+
+
+def _check_argmax(tokens, logits64, what):
+    """tokens vs the first maximum of fp16(logits64); a differing token must
+    be a near tie in float64."""
+    l16 = logits64.half()
+    want = torch.argmax(l16, dim=1)
+    diff = (tokens != want).nonzero().flatten().tolist()
+    for r in diff:
+        a, b = logits64[r, tokens[r]].item(), logits64[r, want[r]].item()
+        assert abs(a - b) <= 2e-3 * max(1.0, abs(b)), f"{what}: row {r} token {tokens[r]} ({a}) vs {want[r]} ({b})"
+    print(f"{what}: {len(diff)} near-tie rows of {len(tokens)}", flush=True)
+    return len(diff)
+
+
+@pytest.mark.parametrize("rows,hidden,vocab", [(1, 1024, 1000), (17, 4096, 4099), (129, 1024, 2000),
+                                               (300, 256, 777)])
+def test_lm_head_argmax_matches_oracle(gpu, rows, hidden, vocab):
+    """Row counts around the 16-row tiles and the 128-row pass; vocab sizes
+    that are not a multiple of the 256-row workgroup."""
+    x = _randn(gpu, rows, hidden, seed=4)
+    w = _randn(gpu, vocab, hidden, seed=5, scale=0.05)
+    tokens = lm_head_argmax(x, w)
+    torch.cuda.synchronize()
+    want_logits = oracle.lm_head_logits(x.cpu().numpy(), w.cpu().numpy())
+    want = oracle.argmax_first(want_logits)
+    l64 = torch.from_numpy(x.cpu().numpy().astype(np.float64) @ w.cpu().numpy().astype(np.float64).T)
+    got = tokens.cpu()
+    n = _check_argmax(got, l64, f"lm_head_argmax {rows}x{hidden}x{vocab}")
+    assert n <= max(1, rows // 50)
+    assert (got.numpy() == want).mean() >= 0.98
+
+
+def test_lm_head_argmax_ties_nan_and_repeat(gpu):
+    """Two identical vocab rows that are the maximum: the first wins; a NaN
+    logit (inf weights against mixed-sign x) counts as the maximum; the keys
+    buffer is left zero, so repeated calls agree."""
+    rows, hidden, vocab = 40, 1024, 2048
+    x = _randn(gpu, rows, hidden, seed=6)
+    w = _randn(gpu, vocab, hidden, seed=7, scale=0.02)
+    w[516] = (x[3].float() * 0.05).half()
+    w[900] = w[516]  # same tile position (mod 32), same arithmetic
+    t1 = lm_head_argmax(x, w)
+    t2 = lm_head_argmax(x, w)
+    torch.cuda.synchronize()
+    assert t1[3].item() == 516
+    assert torch.equal(t1, t2)
+    w[1500] = float("inf")
+    t3 = lm_head_argmax(x, w)
+    torch.cuda.synchronize()
+    assert (t3 == 1500).all(), t3.tolist()
+    print("ties / NaN / repeat: ok", flush=True)
+
+
+def test_lm_head_argmax_qwen3_8b_vocab_vs_reference_formulation(gpu):
+    """Full Qwen3-8B lm_head (151,936 x 4096) at the verify batch (16
+    requests x 5 rows): against float64 logits, and against the reference's
+    own formulation on the same GPU (F.linear then torch.argmax)."""
+    rows, hidden, vocab = 80, 4096, 151936
+    x = _randn(gpu, rows, hidden, seed=8)
+    w = _randn(gpu, vocab, hidden, seed=9, scale=0.02)
+    tokens = lm_head_argmax(x, w)
+    ref = torch.argmax(F.linear(x, w), dim=1)
+    l64 = x.double() @ w.double().T
+    torch.cuda.synchronize()
+    n = _check_argmax(tokens.cpu(), l64.cpu(), "qwen3-8b lm_head")
+    assert n <= 2
+    same = (tokens == ref).float().mean().item()
+    print(f"vs F.linear + argmax: {same:.4f} identical", flush=True)
+    assert same >= 0.95
+
+
+def test_argmax_rows_matches_torch(gpu):
+    """Over given fp16 logits the argmax is bit-exact: ties, NaN, -0/+0,
+    infinities, and a 151,936-wide row."""
+    rows = torch.tensor([[1, 3, 3, 2], [-0.0, 0.0, -1, -2], [float("nan"), 5, 6, 7], [1, float("nan"), float("nan"), 9],
+                         [-float("inf"), -float("inf"), -5, -5], [float("inf"), 1, float("inf"), 0]],
+                        dtype=torch.float16, device=gpu)
+    assert argmax_rows(rows).tolist() == [1, 0, 0, 1, 2, 0]
+    big = _randn(gpu, 50, 151936, seed=10)
+    big[::7, -1] = 100.0
+    big[::5, 77] = 100.0
+    got = argmax_rows(big)
+    assert torch.equal(got, torch.argmax(big, dim=1))
+    assert torch.equal(got.cpu(), torch.from_numpy(oracle.argmax_first(big.cpu().numpy())))
+
+
+def test_post_layer_forward_matches_oracle(gpu):
+    """post_layer.py:49-79 on an infer state with two prompts and decode rows."""
+    from nebulasd_amd.config import QWEN3_0_6B, ModelConfig
+    from nebulasd_amd.infer_state import build_infer_state, rope_cache
+
+    mc = ModelConfig(QWEN3_0_6B)
+    cos, sin = rope_cache(128, mc.rope_theta, 512, gpu)
+    st = build_infer_state([0, 1, 2, 3, 4], [40, 41, 90], [7, 12], mc, cos, sin, gpu)
+    hidden, vocab = 1024, 3000
+    x = _randn(gpu, st.num_tokens, hidden, seed=11)
+    fn = (torch.rand(hidden, device=gpu) + 0.5).half()
+    w = _randn(gpu, vocab, hidden, seed=12, scale=0.05)
+    tokens = post_layer_forward(x, st, fn, w, 1e-6)
+    idx = last_token_indices(st).cpu().numpy()
+    assert idx.tolist() == oracle.last_token_indices([0, 7], [7, 12], 19, 22).tolist()
+    want, logits = oracle.post_layer(x.cpu().numpy(), idx, fn.cpu().numpy(), w.cpu().numpy(), 1e-6)
+    got = tokens.cpu().numpy()
+    assert got.shape == (st.batch_size,)
+    assert (got == want).mean() >= 0.8 and all(
+        abs(float(logits[i, got[i]]) - float(logits[i, want[i]])) <= 2e-2 for i in range(len(got)))

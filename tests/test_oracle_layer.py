@@ -1,0 +1,97 @@
+"""Pins for the rest-of-layer oracle (CPU only): torch's own functional
+routines, closed forms, known answers, and planted mistakes the pins reject."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+
+def _h(rng, *shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float16)
+
+
+def test_fused_add_rmsnorm_matches_torch():
+    rng = np.random.default_rng(0)
+    x, r, w = _h(rng, 7, 4096), _h(rng, 7, 4096), (rng.random(4096) + 0.5).astype(np.float16)
+    out, res = oracle.fused_add_rmsnorm(x, r, w, 1e-6)
+    want_res = (torch.from_numpy(x) + torch.from_numpy(r)).numpy()  # torch's fp16 add
+    np.testing.assert_array_equal(res, want_res)
+    want = F.rms_norm(torch.from_numpy(res).double(), (4096,), torch.from_numpy(w).double(), 1e-6)
+    np.testing.assert_allclose(out.astype(np.float64), want.numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_fused_add_rmsnorm_constant_row_closed_form():
+    x = np.full((2, 64), 1.5, np.float16)
+    r = np.full((2, 64), -0.25, np.float16)
+    w = np.linspace(0.5, 2, 64).astype(np.float16)
+    out, res = oracle.fused_add_rmsnorm(x, r, w, 0.0)
+    assert (res == np.float16(1.25)).all()
+    np.testing.assert_array_equal(out, np.broadcast_to(w, out.shape))  # c / sqrt(c^2) = 1 -> the weights
+
+
+def test_fused_add_rmsnorm_rejects_planted_mistake():
+    rng = np.random.default_rng(1)
+    x, r, w = _h(rng, 3, 256), _h(rng, 3, 256), np.ones(256, np.float16)
+    out, res = oracle.fused_add_rmsnorm(x, r, w, 1e-6)
+    wrong = oracle.rmsnorm_rows(x, w, 1e-6)  # norm of x alone
+    assert np.abs(out.astype(np.float64) - wrong.astype(np.float64)).max() > 0.1
+
+
+def test_silu_and_mul_matches_torch():
+    rng = np.random.default_rng(2)
+    x = _h(rng, 9, 2 * 768, scale=3.0)
+    got = oracle.silu_and_mul(x)
+    t = torch.from_numpy(x).double()
+    gate = F.silu(t[:, 768:]).half().double()  # x * sigmoid(x): another float64 rounding path
+    want = (t[:, :768] * gate).half().numpy()
+    np.testing.assert_allclose(got.astype(np.float64), want.astype(np.float64), rtol=2e-3, atol=1e-6)
+    assert (got == want).mean() > 0.995  # differences only where the fp16 rounding of silu is a near tie
+
+
+def test_silu_and_mul_closed_forms_and_planted_swap():
+    x = np.zeros((1, 16), np.float16)
+    x[0, :8] = np.float16(3.0)      # up
+    x[0, 8:12] = np.float16(0.0)    # gate 0 -> silu 0
+    x[0, 12:] = np.float16(20.0)    # gate large -> silu(g) ~ g
+    got = oracle.silu_and_mul(x)[0]
+    assert (got[:4] == 0).all()
+    np.testing.assert_allclose(got[4:].astype(np.float64), 60.0, rtol=1e-3)
+    swapped = oracle.silu_and_mul(np.concatenate([x[:, 8:], x[:, :8]], axis=1))[0]
+    assert not np.array_equal(swapped, got)
+
+
+def test_argmax_first_known_answers_and_torch():
+    rows = np.array([[1, 3, 3, 2], [-0.0, 0.0, -1, -2], [np.nan, 5, 6, 7], [1, np.nan, np.nan, 9],
+                     [-np.inf, -np.inf, -5, -5]], np.float16)
+    assert oracle.argmax_first(rows).tolist() == [1, 0, 0, 1, 2]
+    assert torch.argmax(torch.from_numpy(rows), dim=1).tolist() == [1, 0, 0, 1, 2]
+    rng = np.random.default_rng(3)
+    big = _h(rng, 40, 5000)
+    big[::3, 4999] = big[::3].max(axis=1) + 1  # maxima at the last column too
+    np.testing.assert_array_equal(oracle.argmax_first(big), torch.argmax(torch.from_numpy(big), dim=1).numpy())
+
+
+def test_last_token_indices_known_answer():
+    # prompts of 3 and 5 tokens, then 2 decode rows -> [2, 7, 8, 9]
+    assert oracle.last_token_indices([0, 3], [3, 5], 8, 10).tolist() == [2, 7, 8, 9]
+    assert oracle.last_token_indices([], [], 0, 4).tolist() == [0, 1, 2, 3]
+
+
+def test_lm_head_logits_and_post_layer_match_torch():
+    rng = np.random.default_rng(4)
+    x = _h(rng, 12, 256)
+    w = _h(rng, 1000, 256, scale=0.1)
+    fn = (rng.random(256) + 0.5).astype(np.float16)
+    idx = [2, 5, 11]
+    tokens, logits = oracle.post_layer(x, idx, fn, w, 1e-6)
+    last = F.rms_norm(torch.from_numpy(x[idx]).double(), (256,), torch.from_numpy(fn).double(), 1e-6).half()
+    want = F.linear(last.double(), torch.from_numpy(w).double()).half()
+    np.testing.assert_allclose(logits.astype(np.float64), want.double().numpy(), rtol=2e-3, atol=2e-3)
+    top2 = np.sort(want.double().numpy(), axis=1)[:, -2:]
+    clear = top2[:, 1] - top2[:, 0] > 1e-2
+    np.testing.assert_array_equal(tokens[clear], torch.argmax(want, dim=1).numpy()[clear])
