@@ -48,6 +48,7 @@ def parse_args():
                    help="comma-separated prefill-attention workloads ('' to skip)")
     p.add_argument("--block-table", type=int, default=1, help="1: time the block-table metadata writer")
     p.add_argument("--hostkv", type=int, default=1, help="1: time the HostKV block-range copies")
+    p.add_argument("--layer-rest", type=int, default=1, help="1: time the rest-of-layer kernels")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -506,6 +507,133 @@ def measure_hostkv(seed: int, reps: int = 6):
                      "legs in alternating order; bytes compared in a separate untimed pass per leg" % reps)}
 
 
+def measure_layer_rest(seed: int, reps: int = 50):
+    """The rest of the layer around the attention path, each kernel beside the
+    reference's formulation on the same GPU (median of `reps` event-timed
+    calls after warmup):
+
+    * lm_head + argmax (post_layer.py:68-69: F.linear then torch.argmax) at
+      the target-verify batch (16 requests x 5 rows, Qwen3-8B lm_head
+      151,936 x 4096) and the draft batch (64 rows, Qwen3-0.6B 151,936 x 1024);
+      algorithmic bytes = the lm_head weight, read once;
+    * fused add-RMSNorm (rmsnorm.py:39-89) and SiLU-and-mul
+      (silu_and_mul.py:5-34) at the verify batch (80 tokens) and a prefill
+      chunk (8,192 tokens), Qwen3-8B widths; algorithmic bytes = every element
+      read and written once.
+
+    Eager figures (`us_per_call`) are `inner` calls back to back between two
+    events for both legs; `us_per_call_graph` replays this build's calls from
+    a HIP graph (device time without launch gaps), which `hbm_gbps` uses for
+    the element-wise kernels."""
+    import itertools
+
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from nebulasd_amd.kernels import fused_add_rmsnorm_inplace, lm_head_argmax, silu_and_mul_inplace
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, inner=10):
+        """µs per call, eager: `inner` calls back to back between two events
+        (median over `reps` groups).  Small kernels are launch-bound here, as
+        the reference's eager layer is."""
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(max(3, reps // inner)):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(inner):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / inner)
+        return float(np.median(ts))
+
+    gstream = torch.cuda.Stream()
+
+    def graph_us(fn, calls=20):
+        """µs per call of this build's kernels replayed from a HIP graph on a
+        side stream (no launch gaps; these kernels record no memset).  The
+        warm-up runs on that stream, so per-stream buffers exist before the
+        capture."""
+        with torch.cuda.stream(gstream):
+            mean, per = _time_graph(lambda: [fn() for _ in range(calls)], gstream, 20, 3)
+        return float(np.median(per)) / calls
+
+    out = {}
+    for name, rows, hidden in (("lm_head_argmax_target_verify", 80, 4096), ("lm_head_argmax_draft_decode", 64, 1024)):
+        vocab = 151936
+        x = (torch.randn(rows, hidden, device=dev, generator=g)).half()
+        w = (torch.randn(vocab, hidden, device=dev, generator=g) * 0.02).half()
+        ours = timed(lambda: lm_head_argmax(x, w))
+        ref = timed(lambda: torch.argmax(F.linear(x, w), dim=1))
+        ours_graph = graph_us(lambda: lm_head_argmax(x, w), calls=4)
+        same = float((lm_head_argmax(x, w) == torch.argmax(F.linear(x, w), dim=1)).float().mean().item())
+        nbytes = vocab * hidden * 2
+        out[name] = {"rows": rows, "hidden": hidden, "vocab": vocab, "us_per_call": ours,
+                     "us_per_call_graph": ours_graph,
+                     "reference_us_per_call": ref, "speedup_vs_reference": ref / ours,
+                     "hbm_gbps": nbytes / ours / 1e3, "identical_tokens_vs_reference": same,
+                     "roofline": {"bound": "hbm", "achieved": nbytes / ours / 1e3, "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": nbytes / ours / 1e3 / HBM_PEAK_GBPS}}
+        del x, w
+    torch.cuda.empty_cache()
+    hidden, inter = 4096, 12288
+    for tokens in (80, 8192):
+        # three (x, residual) sets used in turn: 402 MB at 8,192 tokens, more
+        # than the 256 MB MALL, so each call reads HBM
+        sets = [(torch.randn(tokens, hidden, device=dev, generator=g).half(),
+                 torch.randn(tokens, hidden, device=dev, generator=g).half()) for _ in range(3)]
+        wn = (torch.rand(hidden, device=dev, generator=g) + 0.5).half()
+        turn = itertools.cycle(range(3))
+
+        def ours_norm():
+            x, r = sets[next(turn)]
+            fused_add_rmsnorm_inplace(x, r, wn, 1e-6)
+
+        def ref_norm():
+            x, r = sets[next(turn)]
+            r.add_(x)
+            x.copy_(F.rms_norm(r.float(), (hidden,), wn.float(), 1e-6).half())
+        ours = timed(ours_norm)
+        ours_graph = graph_us(ours_norm, calls=21)
+        ref = timed(ref_norm)
+        nbytes = 4 * tokens * hidden * 2
+        out[f"fused_add_rmsnorm_{tokens}_tokens"] = {
+            "us_per_call": ours, "us_per_call_graph": ours_graph, "reference_us_per_call": ref,
+            "speedup_vs_reference": ref / ours, "hbm_gbps": nbytes / ours_graph / 1e3}
+        # two buffers used in turn (804 MB at 8,192 tokens); the gate half is
+        # centred near 1.3 so repeated in-place calls keep the up half finite
+        ugs = [torch.randn(tokens, 2 * inter, device=dev, generator=g).half() for _ in range(2)]
+        for ug in ugs:
+            ug[:, inter:] = 1.28
+        sturn = itertools.cycle(range(2))
+
+        def ours_silu():
+            silu_and_mul_inplace(ugs[next(sturn)])
+
+        def ref_silu():
+            ug = ugs[next(sturn)]
+            ug[:, :inter] = ug[:, :inter] * F.silu(ug[:, inter:].float()).half()
+        ours_s = timed(ours_silu)
+        ref_s = timed(ref_silu)
+        ours_g = graph_us(ours_silu)
+        nbytes = tokens * inter * 2 * 3
+        out[f"silu_and_mul_{tokens}_tokens"] = {
+            "us_per_call": ours_s, "us_per_call_graph": ours_g, "reference_us_per_call": ref_s,
+            "speedup_vs_reference": ref_s / ours_s, "hbm_gbps": nbytes / ours_g / 1e3}
+        del sets, ugs
+    torch.cuda.empty_cache()
+    return {"workload": "layer_rest", "kind": "rest_of_layer", **out}
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch for `workload`, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy
@@ -636,6 +764,19 @@ def main():
         r2 = measure_block_table(args.seed)
         print(f"# block table bank switch: {r2['us_per_write']:.1f} us per write "
               f"(reference formulation {r2['reference_us_per_write']:.1f} us)", file=sys.stderr, flush=True)
+        secondary[r2["workload"]] = r2
+    if args.layer_rest:
+        r2 = measure_layer_rest(args.seed)
+        print("# rest of layer: lm_head+argmax verify %.1f us (reference %.1f), draft %.1f us (reference %.1f); "
+              "add-rmsnorm 8192 tok %.1f us (reference %.1f); silu-mul 8192 tok %.1f us (reference %.1f)" % (
+                  r2["lm_head_argmax_target_verify"]["us_per_call"],
+                  r2["lm_head_argmax_target_verify"]["reference_us_per_call"],
+                  r2["lm_head_argmax_draft_decode"]["us_per_call"],
+                  r2["lm_head_argmax_draft_decode"]["reference_us_per_call"],
+                  r2["fused_add_rmsnorm_8192_tokens"]["us_per_call"],
+                  r2["fused_add_rmsnorm_8192_tokens"]["reference_us_per_call"],
+                  r2["silu_and_mul_8192_tokens"]["us_per_call"],
+                  r2["silu_and_mul_8192_tokens"]["reference_us_per_call"]), file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.hostkv:
         r2 = measure_hostkv(args.seed)

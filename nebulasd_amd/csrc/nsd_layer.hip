@@ -148,92 +148,105 @@ argmax_rows_kernel(const f16* __restrict__ logits, int64_t vocab, int64_t* token
 
 // ---- lm_head GEMV + argmax -----------------------------------------------
 
-constexpr int kLmWaves = 8;
-constexpr int kLmThreads = kLmWaves * kWave;
-constexpr int kLmTilesPerWave = 2;                         // 16-row vocab tiles per wave
-constexpr int kLmVocabPerWg = kLmWaves * kLmTilesPerWave * 16;  // 256
-constexpr int kLmK = 128;                                  // k-chunk staged per step
-constexpr int kLmRowBytes = kLmK * 2 + 16;                 // 272: rows 4 banks apart
+constexpr int kLmK = 128;                                       // k-chunk per step
+constexpr int kLmRowBytes = kLmK * 2 + 16;                      // 272: rows 4 banks apart
+constexpr int kLmMaxRowTiles = 8;                               // <= 128 rows of x per pass
 
 template <int NRT>
 constexpr int lm_lds_bytes() { return 2 * NRT * 16 * kLmRowBytes; }
 
-// x chunk [NRT*16 rows][kLmK] -> LDS; rows >= n_rows are not written (their
-// columns are never read back).  16 bytes per thread per pass.
-template <int NRT>
-__device__ inline void stage_x(lds_char* dst, const f16* x, int n_rows, int hidden, int k0) {
-  constexpr int kVecs = NRT * 16 * (kLmK / 8);
-  for (int i = threadIdx.x; i < kVecs; i += kLmThreads) {
-    const int r = i / (kLmK / 8), c = i % (kLmK / 8);
-    if (r < n_rows) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(x + (int64_t)r * hidden + k0 + c * 8);
-      *reinterpret_cast<lds_u32x4*>(dst + r * kLmRowBytes + c * 16) = v;
-    }
-  }
-}
-
-// Workgroup: 256 vocab rows (8 waves x 2 tiles of 16) against NRT*16 rows of
-// x.  Lane (i, g) of a wave loads 64 contiguous bytes of W row (tile row i),
-// k = k0 + 32g .. 32g+31, and feeds them to the 4 MFMA steps s as elements
-// 32g + 8s .. +7; the x fragment of row (rt*16 + i) uses the same k order,
-// so every step's dot products cover the chunk exactly once.
-template <int NRT>
-__global__ void __launch_bounds__(kLmThreads)
+// Workgroup: NW*TPW*16 vocab rows (NW waves x TPW tiles of 16) against
+// NRT*16 rows of x.  MFMA step s of chunk k0 covers k = k0 + 32s .. +31: lane (i, g) loads
+// W row (tile row i) elements 32s + 8g .. +7, so the 4 lanes of a row read
+// 64 contiguous bytes per load instruction (whole 64-byte segments), and the
+// x fragment of row (rt*16 + i) is the same 8 elements from LDS.
+//
+// Pipeline per chunk c: x of chunk c+1 is loaded into registers first, then
+// W of chunk c+1, then chunk c's MFMAs run (x from LDS, W from registers),
+// then the x registers go to the other LDS buffer.  Loads complete in
+// order, so that LDS store waits for the x loads only and the weight loads
+// stay in flight across the MFMAs and the barrier.
+template <int NRT, int TPW, int NW, int WPE>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden,
                       int64_t vocab, uint64_t* __restrict__ keys) {
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   lds_char* lds = (lds_char*)lds_raw;
-  __shared__ uint64_t s_best[kLmWaves][NRT * 16];
+  constexpr int kLmThreads = NW * kWave;
+  __shared__ uint64_t s_best[NW][NRT * 16];
+  constexpr int kBuf = NRT * 16 * kLmRowBytes;
+  constexpr int kXRowStep = kLmThreads / (kLmK / 8);      // x rows one pass of the workgroup covers
+  constexpr int kXv = (NRT * 16 + kXRowStep - 1) / kXRowStep;  // 16-byte x vectors per thread per chunk
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int64_t vbase = (int64_t)blockIdx.x * kLmVocabPerWg + wv * (kLmTilesPerWave * 16);
-  const gbl_u32x4* wp[kLmTilesPerWave];
-  bool wok[kLmTilesPerWave];
+  const int64_t vbase = (int64_t)blockIdx.x * (NW * TPW * 16) + wv * (TPW * 16);
+  const gbl_u32x4* wp[TPW];
+  bool wok[TPW];
 #pragma unroll
-  for (int a = 0; a < kLmTilesPerWave; ++a) {
+  for (int a = 0; a < TPW; ++a) {
     const int64_t v = vbase + a * 16 + li;
     wok[a] = v < vocab;
-    wp[a] = (const gbl_u32x4*)(uintptr_t)(w + (wok[a] ? v : 0) * (int64_t)hidden + lg * 32);
+    wp[a] = (const gbl_u32x4*)(uintptr_t)(w + (wok[a] ? v : 0) * (int64_t)hidden + lg * 8);
   }
-  f32x4 acc[kLmTilesPerWave][NRT];
+  // x vector j of this thread: row xr0 + j*kXRowStep of the chunk, 16-byte
+  // column threadIdx.x % 16.
+  const int xc = threadIdx.x % (kLmK / 8), xr0 = threadIdx.x / (kLmK / 8);
+  auto load_x = [&](u32x4 (&xv)[kXv], int k0) {
 #pragma unroll
-  for (int a = 0; a < kLmTilesPerWave; ++a)
+    for (int j = 0; j < kXv; ++j)
+      if (xr0 + j * kXRowStep < n_rows)
+        xv[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(xr0 + j * kXRowStep) * hidden + k0 + xc * 8);
+  };
+  auto store_x = [&](lds_char* dst, const u32x4 (&xv)[kXv]) {
+#pragma unroll
+    for (int j = 0; j < kXv; ++j)
+      if (xr0 + j * kXRowStep < n_rows)
+        *reinterpret_cast<lds_u32x4*>(dst + (xr0 + j * kXRowStep) * kLmRowBytes + xc * 16) = xv[j];
+  };
+  auto load_w = [&](u32x4 (&wr)[TPW][4], int c) {
+#pragma unroll
+    for (int a = 0; a < TPW; ++a)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        wr[a][s] = wok[a] ? __builtin_nontemporal_load(wp[a] + c * (kLmK / 8) + s * 4) : u32x4{0, 0, 0, 0};
+  };
+
+  f32x4 acc[TPW][NRT];
+#pragma unroll
+  for (int a = 0; a < TPW; ++a)
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) acc[a][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int chunks = hidden / kLmK;
-  u32x4 wcur[kLmTilesPerWave][4], wnext[kLmTilesPerWave][4];
-#pragma unroll
-  for (int a = 0; a < kLmTilesPerWave; ++a)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) wcur[a][s] = wok[a] ? __builtin_nontemporal_load(wp[a] + s) : u32x4{0, 0, 0, 0};
-  stage_x<NRT>(lds, x, n_rows, hidden, 0);
+  u32x4 xv[kXv];
+  u32x4 wcur[TPW][4], wnext[TPW][4];
+  load_x(xv, 0);
+  load_w(wcur, 0);
+  store_x(lds, xv);
   __syncthreads();
   for (int c = 0; c < chunks; ++c) {
-    lds_char* cur = lds + (c & 1) * (NRT * 16 * kLmRowBytes);
-    lds_char* nxt = lds + ((c + 1) & 1) * (NRT * 16 * kLmRowBytes);
-    if (c + 1 < chunks) {
-#pragma unroll
-      for (int a = 0; a < kLmTilesPerWave; ++a)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          wnext[a][s] = wok[a] ? __builtin_nontemporal_load(wp[a] + (c + 1) * (kLmK / 8) + s) : u32x4{0, 0, 0, 0};
-      stage_x<NRT>(nxt, x, n_rows, hidden, (c + 1) * kLmK);
+    const lds_char* cur = lds + (c & 1) * kBuf;
+    lds_char* nxt = lds + ((c + 1) & 1) * kBuf;
+    const bool more = c + 1 < chunks;
+    if (more) {
+      load_x(xv, (c + 1) * kLmK);
+      load_w(wnext, c + 1);
     }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-      const lds_char* xb = cur + (rt * 16 + li) * kLmRowBytes + lg * 64;
+      const lds_char* xb = cur + (rt * 16 + li) * kLmRowBytes + lg * 16;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const f16x8 bx = as_h8(*reinterpret_cast<const lds_u32x4*>(xb + s * 16));
+        const f16x8 bx = as_h8(*reinterpret_cast<const lds_u32x4*>(xb + s * 64));
 #pragma unroll
-        for (int a = 0; a < kLmTilesPerWave; ++a) acc[a][rt] = mfma_k32(as_h8(wcur[a][s]), bx, acc[a][rt]);
+        for (int a = 0; a < TPW; ++a) acc[a][rt] = mfma_k32(as_h8(wcur[a][s]), bx, acc[a][rt]);
       }
     }
-    __syncthreads();  // every wave is done with `cur` before it is refilled
-    if (c + 1 < chunks) {
+    if (more) store_x(nxt, xv);  // `nxt` was last read in chunk c-1, before the previous barrier
+    __syncthreads();
+    if (more) {
 #pragma unroll
-      for (int a = 0; a < kLmTilesPerWave; ++a)
+      for (int a = 0; a < TPW; ++a)
 #pragma unroll
         for (int s = 0; s < 4; ++s) wcur[a][s] = wnext[a][s];
     }
@@ -243,7 +256,7 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
   for (int rt = 0; rt < NRT; ++rt) {
     uint64_t best = 0;
 #pragma unroll
-    for (int a = 0; a < kLmTilesPerWave; ++a)
+    for (int a = 0; a < TPW; ++a)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t v = vbase + a * 16 + 4 * lg + e;
@@ -257,21 +270,40 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
   for (int r = threadIdx.x; r < n_rows; r += kLmThreads) {
     uint64_t best = 0;
 #pragma unroll
-    for (int q = 0; q < kLmWaves; ++q) best = umax64(best, s_best[q][r]);
+    for (int q = 0; q < NW; ++q) best = umax64(best, s_best[q][r]);
     if (best) atomicMax(reinterpret_cast<unsigned long long*>(keys + r), (unsigned long long)best);
   }
 }
 
+// Per row-tile count (1..8): vocab tiles per wave, waves per workgroup and
+// the waves per SIMD the register budget is fitted to.  Measured on MI355X
+// over 1..128 rows of the 151,936 x 4096 and x 1024 lm_heads; every entry
+// compiles without spills.  Two vocab tiles per wave halve the x traffic
+// from LDS per weight byte while the row tiles leave registers for three or
+// four waves per SIMD; beyond five row tiles one tile per wave and
+// eight-wave workgroups (128 vocab rows per x chunk staged) win.
+struct LmCfg { int tpw, nw, wpe; };
+constexpr LmCfg kLmTable[kLmMaxRowTiles] = {{2, 4, 4}, {2, 4, 4}, {2, 4, 4}, {2, 4, 3},
+                                            {2, 4, 3}, {1, 8, 3}, {1, 8, 3}, {1, 8, 3}};
+
 template <int NRT>
 void launch_lm(const f16* x, const f16* w, int rows, int hidden, int64_t vocab, uint64_t* keys, hipStream_t s) {
+  constexpr int TPW = kLmTable[NRT - 1].tpw, NW = kLmTable[NRT - 1].nw, WPE = kLmTable[NRT - 1].wpe;
   static bool attr = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_kernel<NRT>),
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_kernel<NRT, TPW, NW, WPE>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, lm_lds_bytes<NRT>()) == hipSuccess;
   }();
   (void)attr;
-  const unsigned grid = (unsigned)((vocab + kLmVocabPerWg - 1) / kLmVocabPerWg);
-  hipLaunchKernelGGL(lm_head_argmax_kernel<NRT>, dim3(grid), dim3(kLmThreads), lm_lds_bytes<NRT>(), s, x, w, rows,
-                     hidden, vocab, keys);
+  constexpr int kVocabPerWg = NW * TPW * 16;
+  const unsigned grid = (unsigned)((vocab + kVocabPerWg - 1) / kVocabPerWg);
+  hipLaunchKernelGGL((lm_head_argmax_kernel<NRT, TPW, NW, WPE>), dim3(grid), dim3(NW * 64), lm_lds_bytes<NRT>(), s,
+                     x, w, rows, hidden, vocab, keys);
+}
+
+template <int... N>
+void launch_lm_rows(std::integer_sequence<int, N...>, int nrt, const f16* x, const f16* w, int rows, int hidden,
+                    int64_t vocab, uint64_t* keys, hipStream_t s) {
+  ((nrt == N + 1 ? launch_lm<N + 1>(x, w, rows, hidden, vocab, keys, s) : void()), ...);
 }
 
 }  // namespace
@@ -332,15 +364,14 @@ extern "C" int nsd_lm_head_argmax(const void* x, const void* lm_head, int64_t n_
   const hipStream_t s = as_stream(stream);
   const f16* xp = static_cast<const f16*>(x);
   const f16* wp = static_cast<const f16*>(lm_head);
-  // Rows in passes of at most 128 (each pass streams the weight once).
+  // Rows in passes of at most 128 (each pass streams the weight once), each
+  // pass with as many 16-row tiles as it needs.
   for (int64_t r0 = 0; r0 < n_rows; r0 += 128) {
     const int rows = (int)std::min<int64_t>(128, n_rows - r0);
     const f16* xr = xp + r0 * hidden;
     uint64_t* kr = keys + r0;
-    if (rows <= 16) launch_lm<1>(xr, wp, rows, (int)hidden, vocab, kr, s);
-    else if (rows <= 32) launch_lm<2>(xr, wp, rows, (int)hidden, vocab, kr, s);
-    else if (rows <= 64) launch_lm<4>(xr, wp, rows, (int)hidden, vocab, kr, s);
-    else launch_lm<8>(xr, wp, rows, (int)hidden, vocab, kr, s);
+    launch_lm_rows(std::make_integer_sequence<int, kLmMaxRowTiles>{}, (rows + 15) / 16, xr, wp, rows, (int)hidden,
+                   vocab, kr, s);
     if (int e = launch_status("lm_head_argmax")) return e;
   }
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)((n_rows + 255) / 256)), dim3(256), 0, s, keys, tokens,
