@@ -11,9 +11,14 @@ this package's gfx950 kernels:
   prefill ``store_kvcache`` and the prompts' causal attention in one launch
   (``flash_attn_varlen_func``, the entry point of transformer_layer.py:7-32
   and :151-164);
-* the rest of the layer (projections, MLP, norms, lm_head) is plain torch, as
-  in the reference (kernels/linear.py:3-12); weights are random (no
-  checkpoints are available offline).
+* the rest of the layer in the reference's order
+  (transformer_layer.py:83-201, model.py:266-301): the residual buffer with
+  ``fused_add_rmsnorm_inplace`` before attention and before the FFN, the
+  stacked up/gate GEMM with ``silu_and_mul_inplace``, and the post-layer's
+  last-token norm with the fused lm_head + argmax (``post_layer_forward``);
+  the GEMMs are library GEMMs through ``F.linear`` as in the reference
+  (kernels/linear.py:3-12).  Weights are random (no checkpoints are
+  available offline).
 
 The loop is NebulaSD's linear speculation: the draft proposes ``depth``
 tokens with single-token decode steps (nebulasd workers/draft/backend.py:52-70);
@@ -43,8 +48,9 @@ import torch.nn.functional as F
 
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from .infer_state import build_infer_state, rope_cache
-from .kernels import (flash_attn_varlen_func, paged_attention, qk_norm_rope_store,
-                      rmsnorm_inplace, rotary_embedding_inplace, store_kvcache)
+from .kernels import (flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention, post_layer_forward,
+                      qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace, silu_and_mul_inplace,
+                      store_kvcache)
 from .speculative import compute_greedy_acceptance
 
 
@@ -68,7 +74,7 @@ class RandomQwen3:
         for _ in range(mc.num_layers):
             self.layers.append(dict(
                 wq=w(hq * d, H), wk=w(hkv * d, H), wv=w(hkv * d, H), wo=w(H, hq * d),
-                wg=w(I, H), wu=w(I, H), wd=w(H, I),
+                wug=w(2 * I, H), wd=w(H, I),  # up rows first, then gate (weight.py:151)
                 n_in=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
                 n_post=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
                 q_norm=(torch.rand(d, device=dev, generator=g) + 0.5).half(),
@@ -90,51 +96,55 @@ class RandomQwen3:
         self.cos, self.sin = rope_cache(d, mc.rope_theta, width * 16 + 1, dev)
         self.check = None  # (layer, callback) of a sampled attention check
 
-    def _norm(self, x, wgt):
-        return F.rms_norm(x.float(), (x.shape[-1],), wgt.float(), self.mc.rms_norm_eps).half()
-
-    def _mlp(self, lw, x):
-        h = self._norm(x, lw["n_post"])
-        return x + F.linear(F.silu(F.linear(h, lw["wg"])) * F.linear(h, lw["wu"]), lw["wd"])
+    def _forward(self, st, token_ids: list, attention) -> list:
+        """transformer_layer.py:83-201 for every layer, then model.py:292 and
+        the post-layer (post_layer.py:49-79); `attention(li, lw, q, k, v)`
+        returns o [tokens, Hq, d].  Returns the greedy token of every request
+        (every prompt's last token, then every decode row)."""
+        mc, dev = self.mc, self.dev
+        eps, inter = mc.rms_norm_eps, mc.ffn_inter_dim
+        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+        x = self.embed[torch.tensor(token_ids, device=dev)]
+        res = torch.zeros_like(x)
+        for li, lw in enumerate(self.layers):
+            fused_add_rmsnorm_inplace(x, res, lw["n_in"], eps)
+            q = F.linear(x, lw["wq"]).view(-1, hq, d)
+            k = F.linear(x, lw["wk"]).view(-1, hkv, d)
+            v = F.linear(x, lw["wv"]).view(-1, hkv, d)
+            o = attention(li, lw, q, k, v)
+            o = F.linear(o.view(x.shape[0], -1), lw["wo"])
+            fused_add_rmsnorm_inplace(o, res, lw["n_post"], eps)
+            up_gate = F.linear(o, lw["wug"])
+            silu_and_mul_inplace(up_gate)
+            x = F.linear(up_gate[:, :inter], lw["wd"])
+        x += res
+        return post_layer_forward(x, st, self.final_norm, self.lm_head, eps).tolist()
 
     def prefill(self, seq_ids: list, prompts: list) -> list:
         """Run the prompts; returns each one's greedy next token."""
         mc, dev = self.mc, self.dev
         lens = [len(p) for p in prompts]
         st = build_infer_state(seq_ids, [], lens, mc, self.cos, self.sin, dev)
-        x = self.embed[torch.tensor([t for p in prompts for t in p], device=dev)]
-        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
-        starts = np.cumsum([0] + lens)
-        for li, lw in enumerate(self.layers):
-            h = self._norm(x, lw["n_in"])
-            q = F.linear(h, lw["wq"]).view(-1, hq, d)
-            k = F.linear(h, lw["wk"]).view(-1, hkv, d)
-            v = F.linear(h, lw["wv"]).view(-1, hkv, d)
+        d = mc.head_dim
+
+        def attention(li, lw, q, k, v):
             rmsnorm_inplace(q.view(-1, d), lw["q_norm"], mc.rms_norm_eps)
             rmsnorm_inplace(k.view(-1, d), lw["k_norm"], mc.rms_norm_eps)
             rotary_embedding_inplace(q, k, st)
             store_kvcache(k, v, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st, li)
-            o = flash_attn_varlen_func(q, k, v, st.prefill_seq_start_locs_with_end,
-                                       st.prefill_seq_start_locs_with_end, st.max_prefill_len,
-                                       st.max_prefill_len, softmax_scale=st.softmax_scale)
-            x = x + F.linear(o.view(x.shape[0], -1), lw["wo"])
-            x = self._mlp(lw, x)
-        last = torch.tensor(starts[1:] - 1, device=dev)
-        logits = F.linear(self._norm(x[last], self.final_norm), self.lm_head)
-        return logits.argmax(-1).tolist()
+            return flash_attn_varlen_func(q, k, v, st.prefill_seq_start_locs_with_end,
+                                          st.prefill_seq_start_locs_with_end, st.max_prefill_len,
+                                          st.max_prefill_len, softmax_scale=st.softmax_scale)
+        return self._forward(st, [t for p in prompts for t in p], attention)
 
     def decode(self, seq_ids: list, seq_lens: list, tokens: list) -> list:
         """Decode / verify rows (rows of one sequence contiguous, seq_lens
         rising by one); returns the greedy next token of every row."""
         mc, dev = self.mc, self.dev
         st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
-        x = self.embed[torch.tensor(tokens, device=dev)]
-        hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
-        for li, lw in enumerate(self.layers):
-            h = self._norm(x, lw["n_in"])
-            q = F.linear(h, lw["wq"]).view(-1, hq, d)
-            k = F.linear(h, lw["wk"]).view(-1, hkv, d)
-            v = F.linear(h, lw["wv"]).view(-1, hkv, d)
+        hq = mc.num_q_heads
+
+        def attention(li, lw, q, k, v):
             qk_norm_rope_store(q, k, v, self.k_cache, self.v_cache, self.block_table,
                                lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin)
             o = torch.empty_like(q)
@@ -147,10 +157,8 @@ class RandomQwen3:
             else:
                 paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
                                 li, o)
-            x = x + F.linear(o.view(x.shape[0], -1), lw["wo"])
-            x = self._mlp(lw, x)
-        logits = F.linear(self._norm(x, self.final_norm), self.lm_head)
-        return logits.argmax(-1).tolist()
+            return o
+        return self._forward(st, tokens, attention)
 
 
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
