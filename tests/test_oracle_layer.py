@@ -95,3 +95,35 @@ def test_lm_head_logits_and_post_layer_match_torch():
     top2 = np.sort(want.double().numpy(), axis=1)[:, -2:]
     clear = top2[:, 1] - top2[:, 0] > 1e-2
     np.testing.assert_array_equal(tokens[clear], torch.argmax(want, dim=1).numpy()[clear])
+
+
+def test_capi_argument_checks_without_gpu():
+    """The rest-of-layer entry points reject bad shapes and pointers before
+    any HIP call, and return success with nothing to do."""
+    from nebulasd_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from nebulasd_amd.build import build
+
+        build()
+    lib = _lib.load()
+    p = 0x10000  # 16-byte aligned, never dereferenced: every call below fails or has nothing to do
+    cases = [
+        (lambda: lib.nsd_fused_add_rmsnorm_inplace(p, p, p, 4, 8200, 1e-6, None), 2, "hidden=8200"),
+        (lambda: lib.nsd_fused_add_rmsnorm_inplace(p, p, p, 4, 12, 1e-6, None), 2, "hidden=12"),
+        (lambda: lib.nsd_fused_add_rmsnorm_inplace(None, p, p, 4, 64, 1e-6, None), 1, "null"),
+        (lambda: lib.nsd_fused_add_rmsnorm_inplace(p + 2, p, p, 4, 64, 1e-6, None), 2, "aligned"),
+        (lambda: lib.nsd_silu_and_mul_inplace(p, 4, 12, None), 2, "inter_dim=12"),
+        (lambda: lib.nsd_silu_and_mul_inplace(None, 4, 16, None), 1, "null"),
+        (lambda: lib.nsd_lm_head_argmax(p, p, 4, 100, 1000, p, p, None), 2, "hidden=100"),
+        (lambda: lib.nsd_lm_head_argmax(p, p, 4, 128, 0, p, p, None), 1, "bad shape"),
+        (lambda: lib.nsd_lm_head_argmax(p, p, 4, 128, 1000, None, p, None), 1, "null"),
+        (lambda: lib.nsd_argmax_rows(p, 4, 0, p, None), 1, "bad shape"),
+    ]
+    for call, code, msg in cases:
+        rc = call()
+        assert rc == code and msg in _lib.last_error(), (rc, code, msg, _lib.last_error())
+    assert lib.nsd_fused_add_rmsnorm_inplace(None, None, None, 0, 4096, 1e-6, None) == 0
+    assert lib.nsd_silu_and_mul_inplace(None, 0, 16, None) == 0
+    assert lib.nsd_lm_head_argmax(None, None, 0, 128, 10, None, None, None) == 0
+    assert lib.nsd_argmax_rows(None, 0, 10, None, None) == 0
