@@ -278,7 +278,7 @@ def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: 
     return res
 
 
-def measure_block_table(seed: int, reps: int = 50):
+def measure_block_table(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
     """Bank-switch metadata: 128 block-table rows get contiguous ranges of
     U[0, 256] blocks.  Host-to-completion latency per write (median over
     `reps`, synchronised) of this build's writer and of the reference's
@@ -336,7 +336,14 @@ def measure_block_table(seed: int, reps: int = 50):
     ref_bt = bt.clone()
     ours()
     same = bool(torch.equal(bt, ref_bt))
-    return {"workload": "block_table_bank_switch", "kind": "metadata", "rows": rows_n,
+    cpu = None
+    if cpu_seconds > 0:
+        import oracle
+
+        btn, nan_ = bt.cpu().numpy(), na.cpu().numpy()
+        cpu = _cpu_time(lambda: oracle.write_block_ranges(btn, rows, begins, counts, nan_), cpu_seconds, 200,
+                        what="the numpy oracle's range writer over the same 128 rows")
+    return {"workload": "block_table_bank_switch", "kind": "metadata", "rows": rows_n, "cpu_baseline": cpu,
             "blocks_written": cap, "us_per_write": out["ours"], "reference_us_per_write": out["reference"],
             "speedup_vs_reference": out["reference"] / out["ours"], "identical_tables": same,
             "note": "host-to-completion latency, median of %d synchronised writes" % reps}
@@ -507,7 +514,7 @@ def measure_hostkv(seed: int, reps: int = 6):
                      "legs in alternating order; bytes compared in a separate untimed pass per leg" % reps)}
 
 
-def measure_layer_rest(seed: int, reps: int = 50):
+def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
     """The rest of the layer around the attention path, each kernel beside the
     reference's formulation on the same GPU (median of `reps` event-timed
     calls after warmup):
@@ -577,7 +584,16 @@ def measure_layer_rest(seed: int, reps: int = 50):
         ours_graph = graph_us(lambda: lm_head_argmax(x, w), calls=4)
         same = float((lm_head_argmax(x, w) == torch.argmax(F.linear(x, w), dim=1)).float().mean().item())
         nbytes = vocab * hidden * 2
-        out[name] = {"rows": rows, "hidden": hidden, "vocab": vocab, "us_per_call": ours,
+        cpu = None
+        if cpu_seconds > 0:
+            import oracle
+
+            xn, wn32 = x.cpu().numpy(), w.cpu().numpy().astype(np.float32)
+            cpu = _cpu_time(lambda: oracle.argmax_first(oracle.lm_head_logits(xn, wn32, np.float32)),
+                            cpu_seconds, what=f"the numpy oracle's lm_head logits (fp32 sums) + argmax, "
+                                              f"{rows} x {hidden} x {vocab}")
+            del wn32
+        out[name] = {"rows": rows, "hidden": hidden, "vocab": vocab, "us_per_call": ours, "cpu_baseline": cpu,
                      "us_per_call_graph": ours_graph,
                      "reference_us_per_call": ref, "speedup_vs_reference": ref / ours,
                      "hbm_gbps": nbytes / ours / 1e3, "identical_tokens_vs_reference": same,
@@ -605,10 +621,17 @@ def measure_layer_rest(seed: int, reps: int = 50):
         ours = timed(ours_norm)
         ours_graph = graph_us(ours_norm, calls=21)
         ref = timed(ref_norm)
+        cpu = None
+        if cpu_seconds > 0:
+            import oracle
+
+            xn, rn, wnn = sets[0][0].cpu().numpy(), sets[0][1].cpu().numpy(), wn.cpu().numpy()
+            cpu = _cpu_time(lambda: oracle.fused_add_rmsnorm(xn, rn, wnn, 1e-6), cpu_seconds,
+                            what=f"the numpy oracle's fused add-RMSNorm, {tokens} x {hidden}")
         nbytes = 4 * tokens * hidden * 2
         out[f"fused_add_rmsnorm_{tokens}_tokens"] = {
             "us_per_call": ours, "us_per_call_graph": ours_graph, "reference_us_per_call": ref,
-            "speedup_vs_reference": ref / ours, "hbm_gbps": nbytes / ours_graph / 1e3}
+            "speedup_vs_reference": ref / ours, "hbm_gbps": nbytes / ours_graph / 1e3, "cpu_baseline": cpu}
         # two buffers used in turn (804 MB at 8,192 tokens); the gate half is
         # centred near 1.3 so repeated in-place calls keep the up half finite
         ugs = [torch.randn(tokens, 2 * inter, device=dev, generator=g).half() for _ in range(2)]
@@ -625,10 +648,17 @@ def measure_layer_rest(seed: int, reps: int = 50):
         ours_s = timed(ours_silu)
         ref_s = timed(ref_silu)
         ours_g = graph_us(ours_silu)
+        cpu = None
+        if cpu_seconds > 0:
+            import oracle
+
+            un = ugs[0].cpu().numpy()
+            cpu = _cpu_time(lambda: oracle.silu_and_mul(un), cpu_seconds,
+                            what=f"the numpy oracle's SiLU-and-mul, {tokens} x {inter}")
         nbytes = tokens * inter * 2 * 3
         out[f"silu_and_mul_{tokens}_tokens"] = {
             "us_per_call": ours_s, "us_per_call_graph": ours_g, "reference_us_per_call": ref_s,
-            "speedup_vs_reference": ref_s / ours_s, "hbm_gbps": nbytes / ours_g / 1e3}
+            "speedup_vs_reference": ref_s / ours_s, "hbm_gbps": nbytes / ours_g / 1e3, "cpu_baseline": cpu}
         del sets, ugs
     torch.cuda.empty_cache()
     return {"workload": "layer_rest", "kind": "rest_of_layer", **out}
@@ -715,6 +745,27 @@ def cpu_baseline(w, budget_s: float):
     }
 
 
+def _cpu_time(fn, budget_s: float, max_reps: int = 20, what: str = "") -> dict:
+    """Median wall time of fn() on the host cores (at most 16 threads), at
+    least one call and about `budget_s` seconds."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    times = []
+    with threadpool_limits(limits=cores):
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        t_end = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end or len(times) >= max_reps:
+                break
+    return {"value": float(np.median(times)) * 1e6, "unit": "us/call", "cores": int(min(threads, cores)),
+            "kind": "port", "sample": f"{len(times)} calls of {what}, median", "cpu_model": _cpu_model()}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -761,12 +812,12 @@ def main():
               f"(reference SDPA loop {r2['reference_sdpa_loop_us']:.0f} us)", file=sys.stderr, flush=True)
         secondary[name] = r2
     if args.block_table:
-        r2 = measure_block_table(args.seed)
+        r2 = measure_block_table(args.seed, cpu_seconds=min(1.0, args.other_cpu_seconds) if args.cpu_baseline_seconds > 0 else 0)
         print(f"# block table bank switch: {r2['us_per_write']:.1f} us per write "
               f"(reference formulation {r2['reference_us_per_write']:.1f} us)", file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.layer_rest:
-        r2 = measure_layer_rest(args.seed)
+        r2 = measure_layer_rest(args.seed, cpu_seconds=args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
         print("# rest of layer: lm_head+argmax verify %.1f us (reference %.1f), draft %.1f us (reference %.1f); "
               "add-rmsnorm 8192 tok %.1f us (reference %.1f); silu-mul 8192 tok %.1f us (reference %.1f)" % (
                   r2["lm_head_argmax_target_verify"]["us_per_call"],

@@ -26,6 +26,8 @@ def _keys(device: torch.device, stream: int, rows: int) -> torch.Tensor:
     k = (device, stream)
     buf = _KEYS.get(k)
     if buf is None or buf.numel() < rows:
+        if buf is None and len(_KEYS) >= 16:
+            _KEYS.clear()  # each dropped buffer is freed in its own stream's order
         buf = torch.zeros(max(rows, 256), dtype=torch.int64, device=device)
         _KEYS[k] = buf
     return buf

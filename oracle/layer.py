@@ -69,10 +69,11 @@ def last_token_indices(prefill_seq_start_locs, prefill_seq_lens, num_prefill_tok
     return np.concatenate([starts + lens - 1, np.arange(num_prefill_tokens, num_tokens, dtype=np.int64)])
 
 
-def lm_head_logits(x, lm_head):
+def lm_head_logits(x, lm_head, dtype=np.float64):
     """layers/post_layer.py:68 (kernels/linear.py:3-12): x @ lm_head^T,
-    float64 sums rounded to fp16."""
-    return (x.astype(np.float64) @ lm_head.astype(np.float64).T).astype(np.float16)
+    sums in `dtype` (float64 for parity; float32 for the timed CPU baseline)
+    rounded to fp16."""
+    return (x.astype(dtype, copy=False) @ lm_head.astype(dtype, copy=False).T).astype(np.float16)
 
 
 def post_layer(input_embds, indices, final_norm, lm_head, eps):
