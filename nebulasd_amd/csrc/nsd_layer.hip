@@ -166,7 +166,7 @@ constexpr int lm_lds_bytes() { return 2 * NRT * 16 * kLmRowBytes; }
 // then the x registers go to the other LDS buffer.  Loads complete in
 // order, so that LDS store waits for the x loads only and the weight loads
 // stay in flight across the MFMAs and the barrier.
-template <int NRT, int TPW, int NW, int WPE>
+template <int NRT, int TPW, int NW, int WPE, int PD>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden,
                       int64_t vocab, uint64_t* __restrict__ keys) {
@@ -219,37 +219,42 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
 
   const int chunks = hidden / kLmK;
   u32x4 xv[kXv];
-  u32x4 wcur[TPW][4], wnext[TPW][4];
+  // Register ring of weight chunks: chunk c computes from wr[c % R] while
+  // chunks c+1 .. c+PD load into the others (static indices: the loop is
+  // unrolled by R, so no register moves wait on loads in flight).
+  constexpr int R = PD + 1;
+  u32x4 wr[R][TPW][4];
   load_x(xv, 0);
-  load_w(wcur, 0);
+  static_for<PD>([&](auto u) {
+    constexpr int k = decltype(u)::value;
+    if (k < chunks) load_w(wr[k], k);
+  });
   store_x(lds, xv);
   __syncthreads();
-  for (int c = 0; c < chunks; ++c) {
-    const lds_char* cur = lds + (c & 1) * kBuf;
-    lds_char* nxt = lds + ((c + 1) & 1) * kBuf;
-    const bool more = c + 1 < chunks;
-    if (more) {
-      load_x(xv, (c + 1) * kLmK);
-      load_w(wnext, c + 1);
-    }
+  for (int c0 = 0; c0 < chunks; c0 += R) {
+    static_for<R>([&](auto u) {
+      constexpr int k = decltype(u)::value;
+      const int c = c0 + k;
+      if (c < chunks) {
+        const lds_char* cur = lds + (c & 1) * kBuf;
+        lds_char* nxt = lds + ((c + 1) & 1) * kBuf;
+        const bool more = c + 1 < chunks;
+        if (more) load_x(xv, (c + 1) * kLmK);
+        if (c + PD < chunks) load_w(wr[(k + PD) % R], c + PD);
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      const lds_char* xb = cur + (rt * 16 + li) * kLmRowBytes + lg * 16;
+        for (int rt = 0; rt < NRT; ++rt) {
+          const lds_char* xb = cur + (rt * 16 + li) * kLmRowBytes + lg * 16;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const f16x8 bx = as_h8(*reinterpret_cast<const lds_u32x4*>(xb + s * 64));
+          for (int s = 0; s < 4; ++s) {
+            const f16x8 bx = as_h8(*reinterpret_cast<const lds_u32x4*>(xb + s * 64));
 #pragma unroll
-        for (int a = 0; a < TPW; ++a) acc[a][rt] = mfma_k32(as_h8(wcur[a][s]), bx, acc[a][rt]);
+            for (int a = 0; a < TPW; ++a) acc[a][rt] = mfma_k32(as_h8(wr[k][a][s]), bx, acc[a][rt]);
+          }
+        }
+        if (more) store_x(nxt, xv);  // `nxt` was last read in chunk c-1, before the previous barrier
+        __syncthreads();
       }
-    }
-    if (more) store_x(nxt, xv);  // `nxt` was last read in chunk c-1, before the previous barrier
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int a = 0; a < TPW; ++a)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) wcur[a][s] = wnext[a][s];
-    }
+    });
   }
   // acc[a][rt][e]: logit of vocab row vbase + a*16 + 4*lg + e, x row rt*16 + li.
 #pragma unroll
@@ -275,28 +280,31 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
   }
 }
 
-// Per row-tile count (1..8): vocab tiles per wave, waves per workgroup and
-// the waves per SIMD the register budget is fitted to.  Measured on MI355X
+// Per row-tile count (1..8): vocab tiles per wave, waves per workgroup, the
+// waves per SIMD the register budget is fitted to, and the weight prefetch
+// distance in chunks (2 measured slower everywhere: it spills or costs a
+// wave per SIMD).  Measured on MI355X
 // over 1..128 rows of the 151,936 x 4096 and x 1024 lm_heads; every entry
 // compiles without spills.  Two vocab tiles per wave halve the x traffic
 // from LDS per weight byte while the row tiles leave registers for three or
 // four waves per SIMD; beyond five row tiles one tile per wave and
 // eight-wave workgroups (128 vocab rows per x chunk staged) win.
-struct LmCfg { int tpw, nw, wpe; };
-constexpr LmCfg kLmTable[kLmMaxRowTiles] = {{2, 4, 4}, {2, 4, 4}, {2, 4, 4}, {2, 4, 3},
-                                            {2, 4, 3}, {1, 8, 3}, {1, 8, 3}, {1, 8, 3}};
+struct LmCfg { int tpw, nw, wpe, pd; };
+constexpr LmCfg kLmTable[kLmMaxRowTiles] = {{2, 4, 4, 1}, {2, 4, 4, 1}, {2, 4, 4, 1}, {2, 4, 3, 1},
+                                            {2, 4, 3, 1}, {1, 8, 3, 1}, {1, 8, 3, 1}, {1, 8, 3, 1}};
 
 template <int NRT>
 void launch_lm(const f16* x, const f16* w, int rows, int hidden, int64_t vocab, uint64_t* keys, hipStream_t s) {
   constexpr int TPW = kLmTable[NRT - 1].tpw, NW = kLmTable[NRT - 1].nw, WPE = kLmTable[NRT - 1].wpe;
+  constexpr int PD = kLmTable[NRT - 1].pd;
   static bool attr = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_kernel<NRT, TPW, NW, WPE>),
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_kernel<NRT, TPW, NW, WPE, PD>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, lm_lds_bytes<NRT>()) == hipSuccess;
   }();
   (void)attr;
   constexpr int kVocabPerWg = NW * TPW * 16;
   const unsigned grid = (unsigned)((vocab + kVocabPerWg - 1) / kVocabPerWg);
-  hipLaunchKernelGGL((lm_head_argmax_kernel<NRT, TPW, NW, WPE>), dim3(grid), dim3(NW * 64), lm_lds_bytes<NRT>(), s,
+  hipLaunchKernelGGL((lm_head_argmax_kernel<NRT, TPW, NW, WPE, PD>), dim3(grid), dim3(NW * 64), lm_lds_bytes<NRT>(), s,
                      x, w, rows, hidden, vocab, keys);
 }
 
