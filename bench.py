@@ -49,6 +49,7 @@ def parse_args():
     p.add_argument("--block-table", type=int, default=1, help="1: time the block-table metadata writer")
     p.add_argument("--hostkv", type=int, default=1, help="1: time the HostKV block-range copies")
     p.add_argument("--layer-rest", type=int, default=1, help="1: time the rest-of-layer kernels")
+    p.add_argument("--layer-step", type=int, default=1, help="1: time one whole target-verify layer")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -514,6 +515,113 @@ def measure_hostkv(seed: int, reps: int = 6):
                      "legs in alternating order; bytes compared in a separate untimed pass per leg" % reps)}
 
 
+def measure_layer_step(seed: int, reps: int = 20):
+    """One whole Qwen3-8B target-verify decoder layer (16 requests x 5 rows,
+    contexts U[256, 4096]) in the reference's order
+    (transformer_layer.py:83-201) on this build's kernels, the GEMMs through
+    F.linear (hipBLASLt): fused add-RMSNorm, q/k/v GEMMs, the fused prologue,
+    paged attention, O GEMM, fused add-RMSNorm, up/gate GEMM, SiLU-and-mul,
+    down GEMM.  Passes of four layers (weights of four distinct layers,
+    1.7 GB, so each layer reads its weights from HBM): the whole layer, the
+    GEMMs alone and the rest alone.  Floor: weight bytes + the attention's
+    K/V bytes at the device-copy rate.  Timed eagerly (see below).""" 
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from nebulasd_amd.config import EngineConfig, ModelConfig
+    from nebulasd_amd.infer_state import build_infer_state, rope_cache
+    from nebulasd_amd.kernels import (fused_add_rmsnorm_inplace, paged_attention, qk_norm_rope_store,
+                                      silu_and_mul_inplace)
+    from nebulasd_amd.workload import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload("target_verify", seed, device=dev)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    cos, sin = rope_cache(128, mc.rope_theta, max(w.seq_lens) + 1, dev)
+    st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, dev)
+    H, I, hq, hkv, d = mc.hidden_size, mc.ffn_inter_dim, mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+    T = w.rows
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+
+    def rnd(*shape, scale=0.02):
+        return (torch.randn(shape, device=dev, generator=g) * scale).half()
+    n_layers = 4
+    layers = [dict(wq=rnd(hq * d, H), wk=rnd(hkv * d, H), wv=rnd(hkv * d, H), wo=rnd(H, hq * d),
+                   wug=rnd(2 * I, H), wd=rnd(H, I), n_in=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                   n_post=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                   qn=(torch.rand(d, device=dev, generator=g) + 0.5).half(),
+                   kn=(torch.rand(d, device=dev, generator=g) + 0.5).half()) for _ in range(n_layers)]
+    weight_bytes = sum(t.numel() * 2 for t in layers[0].values())
+    x0 = rnd(T, H, scale=1.0)
+    x, res = x0.clone(), torch.zeros_like(x0)
+    o = torch.empty((T, hq, d), dtype=torch.float16, device=dev)
+    q = torch.empty_like(o)
+    k = torch.empty((T, hkv, d), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    oo = torch.empty((T, H), dtype=torch.float16, device=dev)
+    ug = torch.empty((T, 2 * I), dtype=torch.float16, device=dev)
+    kv_layer = [mc.num_layers // 2 + i for i in range(n_layers)]
+
+    def layer(i, gemms=True, rest=True):
+        lw = layers[i]
+        if rest:
+            fused_add_rmsnorm_inplace(x, res, lw["n_in"], mc.rms_norm_eps)
+        if gemms:
+            torch.mm(x, lw["wq"].t(), out=q.view(T, -1))
+            torch.mm(x, lw["wk"].t(), out=k.view(T, -1))
+            torch.mm(x, lw["wv"].t(), out=v.view(T, -1))
+        if rest:
+            qk_norm_rope_store(q, k, v, w.k_cache, w.v_cache, w.block_table, lw["qn"], lw["kn"], mc, ec, st,
+                               kv_layer[i], cos, sin)
+            paged_attention(q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, kv_layer[i], o)
+        if gemms:
+            torch.mm(o.view(T, -1), lw["wo"].t(), out=oo)
+        if rest:
+            fused_add_rmsnorm_inplace(oo, res, lw["n_post"], mc.rms_norm_eps)
+        if gemms:
+            torch.mm(oo, lw["wug"].t(), out=ug)
+        if rest:
+            silu_and_mul_inplace(ug)
+        if gemms:
+            torch.mm(ug[:, :I], lw["wd"].t(), out=x)
+
+    # Eager, not a graph: the library GEMMs may record memset nodes, which a
+    # captured graph must not hold.  `reps` passes of four layers are enqueued
+    # back to back between two events; the host's enqueue time is kept too,
+    # so a host-bound figure shows as host_us >= device us.
+    stream = torch.cuda.current_stream()
+    out, host = {}, {}
+    for name, kw in (("layer", {}), ("gemms_only", {"rest": False}), ("rest_only", {"gemms": False})):
+        for i in range(n_layers):
+            layer(i, **kw)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(reps):
+            for i in range(n_layers):
+                layer(i, **kw)
+        e1.record(stream)
+        host[name] = (time.perf_counter() - t0) * 1e6 / (reps * n_layers)
+        e1.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
+    kv_bytes = w.algorithmic_bytes()
+    copy = getattr(measure_layer_step, "copy_gbps", None)
+    floor = (weight_bytes + (kv_bytes or 0)) / (copy * 1e3) if copy and kv_bytes else None
+    del w, layers
+    torch.cuda.empty_cache()
+    return {"workload": "layer_step_target_verify", "kind": "whole_layer", "rows": T,
+            "us_per_layer": out["layer"], "gemms_only_us": out["gemms_only"], "rest_only_us": out["rest_only"],
+            "host_enqueue_us_per_layer": host,
+            "weight_bytes_per_layer": weight_bytes, "kv_bytes_per_layer": kv_bytes,
+            "floor_us_at_copy_rate": floor,
+            "note": "GEMMs through torch.mm (hipBLASLt) with the reference's three q/k/v projections; the rest "
+                    "is this build's kernels; eager passes of four layers with distinct weights"}
+
+
 def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
     """The rest of the layer around the attention path, each kernel beside the
     reference's formulation on the same GPU (median of `reps` event-timed
@@ -815,6 +923,14 @@ def main():
         r2 = measure_block_table(args.seed, cpu_seconds=min(1.0, args.other_cpu_seconds) if args.cpu_baseline_seconds > 0 else 0)
         print(f"# block table bank switch: {r2['us_per_write']:.1f} us per write "
               f"(reference formulation {r2['reference_us_per_write']:.1f} us)", file=sys.stderr, flush=True)
+        secondary[r2["workload"]] = r2
+    if args.layer_step:
+        measure_layer_step.copy_gbps = copy_gbps
+        r2 = measure_layer_step(args.seed)
+        print("# target verify layer: %.1f us (GEMMs alone %.1f, rest alone %.1f; floor %s us)" % (
+            r2["us_per_layer"], r2["gemms_only_us"], r2["rest_only_us"],
+            "%.1f" % r2["floor_us_at_copy_rate"] if r2["floor_us_at_copy_rate"] else "n/a"),
+            file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.layer_rest:
         r2 = measure_layer_rest(args.seed, cpu_seconds=args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
