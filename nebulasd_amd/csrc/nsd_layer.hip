@@ -166,36 +166,40 @@ constexpr int lm_lds_bytes() { return 2 * NRT * 16 * kLmRowBytes; }
 // then the x registers go to the other LDS buffer.  Loads complete in
 // order, so that LDS store waits for the x loads only and the weight loads
 // stay in flight across the MFMAs and the barrier.
-template <int NRT, int TPW, int NW, int WPE, int PD>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
-lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden,
-                      int64_t vocab, uint64_t* __restrict__ keys) {
-  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
-  lds_char* lds = (lds_char*)lds_raw;
+//
+// skinny_mainloop: the wave's weight rows [vbase, vbase + TPW*16) (rows past
+// n_out read as zero) against x rows [0, n_rows) (row stride x_stride) over
+// the k chunks [kc0, kc0 + chunks) of 128; sums accumulate into acc.  Every
+// thread of the workgroup calls it with the same chunk range (it holds
+// barriers).
+template <int NRT, int TPW, int NW, int PD>
+__device__ __forceinline__ void skinny_mainloop(const f16* __restrict__ x, int64_t x_stride,
+                                                const f16* __restrict__ w, int n_rows, int hidden,
+                                                int64_t vbase, int64_t n_out, int kc0, int chunks,
+                                                lds_char* lds, f32x4 (&acc)[TPW][NRT]) {
   constexpr int kLmThreads = NW * kWave;
-  __shared__ uint64_t s_best[NW][NRT * 16];
   constexpr int kBuf = NRT * 16 * kLmRowBytes;
   constexpr int kXRowStep = kLmThreads / (kLmK / 8);      // x rows one pass of the workgroup covers
   constexpr int kXv = (NRT * 16 + kXRowStep - 1) / kXRowStep;  // 16-byte x vectors per thread per chunk
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
-  const int64_t vbase = (int64_t)blockIdx.x * (NW * TPW * 16) + wv * (TPW * 16);
   const gbl_u32x4* wp[TPW];
   bool wok[TPW];
 #pragma unroll
   for (int a = 0; a < TPW; ++a) {
     const int64_t v = vbase + a * 16 + li;
-    wok[a] = v < vocab;
-    wp[a] = (const gbl_u32x4*)(uintptr_t)(w + (wok[a] ? v : 0) * (int64_t)hidden + lg * 8);
+    wok[a] = v < n_out;
+    wp[a] = (const gbl_u32x4*)(uintptr_t)(w + (wok[a] ? v : 0) * (int64_t)hidden + (int64_t)kc0 * kLmK + lg * 8);
   }
   // x vector j of this thread: row xr0 + j*kXRowStep of the chunk, 16-byte
   // column threadIdx.x % 16.
   const int xc = threadIdx.x % (kLmK / 8), xr0 = threadIdx.x / (kLmK / 8);
+  const f16* xk = x + (int64_t)kc0 * kLmK;
   auto load_x = [&](u32x4 (&xv)[kXv], int k0) {
 #pragma unroll
     for (int j = 0; j < kXv; ++j)
       if (xr0 + j * kXRowStep < n_rows)
-        xv[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(xr0 + j * kXRowStep) * hidden + k0 + xc * 8);
+        xv[j] = *reinterpret_cast<const u32x4*>(xk + (int64_t)(xr0 + j * kXRowStep) * x_stride + k0 + xc * 8);
   };
   auto store_x = [&](lds_char* dst, const u32x4 (&xv)[kXv]) {
 #pragma unroll
@@ -211,13 +215,6 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
         wr[a][s] = wok[a] ? __builtin_nontemporal_load(wp[a] + c * (kLmK / 8) + s * 4) : u32x4{0, 0, 0, 0};
   };
 
-  f32x4 acc[TPW][NRT];
-#pragma unroll
-  for (int a = 0; a < TPW; ++a)
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) acc[a][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int chunks = hidden / kLmK;
   u32x4 xv[kXv];
   // Register ring of weight chunks: chunk c computes from wr[c % R] while
   // chunks c+1 .. c+PD load into the others (static indices: the loop is
@@ -256,6 +253,25 @@ lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int 
       }
     });
   }
+}
+
+template <int NRT, int TPW, int NW, int WPE, int PD>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden,
+                      int64_t vocab, uint64_t* __restrict__ keys) {
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  lds_char* lds = (lds_char*)lds_raw;
+  constexpr int kLmThreads = NW * kWave;
+  __shared__ uint64_t s_best[NW][NRT * 16];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int64_t vbase = (int64_t)blockIdx.x * (NW * TPW * 16) + wv * (TPW * 16);
+  f32x4 acc[TPW][NRT];
+#pragma unroll
+  for (int a = 0; a < TPW; ++a)
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) acc[a][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  skinny_mainloop<NRT, TPW, NW, PD>(x, hidden, w, n_rows, hidden, vbase, vocab, 0, hidden / kLmK, lds, acc);
   // acc[a][rt][e]: logit of vocab row vbase + a*16 + 4*lg + e, x row rt*16 + li.
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) {

@@ -127,3 +127,4 @@ def test_capi_argument_checks_without_gpu():
     assert lib.nsd_silu_and_mul_inplace(None, 0, 16, None) == 0
     assert lib.nsd_lm_head_argmax(None, None, 0, 128, 10, None, None, None) == 0
     assert lib.nsd_argmax_rows(None, 0, 10, None, None) == 0
+
