@@ -122,6 +122,25 @@ int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w
                            int32_t* status, void* stream);
 
 /*
+ * nsd_qk_norm_rope_store_strided: the same prologue for q/k/v rows that are
+ * slices of one fused projection output [rows, (Hq + 2*Hkv) * d]: row i of
+ * q, k and v starts q_row_stride, k_row_stride, v_row_stride elements after
+ * row i-1 (even, and at least the row's heads x head_dim).  The normalised,
+ * rotated q goes to q_out [rows, Hq, d] contiguous (what nsd_paged_attention
+ * reads); k is rotated in place; K and V go to the cache as above.  One
+ * q/k/v GEMM then replaces the reference's three (transformer_layer.py:107-109).
+ */
+int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_out, void* k,
+                                   int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                   const void* q_norm_w, const void* k_norm_w, float eps,
+                                   const void* cos_cache, const void* sin_cache, int64_t n_positions,
+                                   void* k_cache, void* v_cache, const int32_t* block_table,
+                                   int64_t bt_rows, int64_t bt_stride, const int32_t* seq_ids,
+                                   const int32_t* seq_lens, int64_t n_rows, int64_t num_blocks,
+                                   int num_layers, int layer, int num_q_heads, int num_kv_heads,
+                                   int head_dim, int block_size, int32_t* status, void* stream);
+
+/*
  * Attention work plan (host side, no HIP calls).  The reference picks a
  * split size per forward (swiftLLM/swiftllm/worker/model.py:365-384) and
  * launches one program per (row, q-head, split) (kernels/paged_attn.py:182-211).

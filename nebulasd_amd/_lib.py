@@ -50,6 +50,10 @@ SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
                 c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
                 c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "nsd_qk_norm_rope_store_strided": (
+        c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_float,
+                c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+                c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     "nsd_attn_plan_bound": (c_int64, [c_int64, c_int, c_int]),
     "nsd_attn_plan_build": (
         c_int, [_I32P, _I32P, c_int64, c_int, c_int, c_int, c_int, c_int64, c_int64, c_int, c_int,

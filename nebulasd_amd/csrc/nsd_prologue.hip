@@ -125,11 +125,15 @@ __global__ __launch_bounds__(256) void rope_kernel(f16* __restrict__ q, f16* __r
 }
 
 // Fused prologue: one wave per (row, head) over heads [q heads | k heads | v heads].
-// q/k heads: rmsnorm (fp32, fp16 store) -> RoPE at seq_len-1 -> in place;
-// k heads also write the rotated row to the cache slot; v heads copy to it.
-// Order and math of transformer_layer.py:114-145 in one launch.
+// q/k heads: rmsnorm (fp32, fp16 store) -> RoPE at seq_len-1; k in place, q
+// into q_out (q itself, or a contiguous buffer when q is a strided slice of a
+// fused q/k/v projection); k heads also write the rotated row to the cache
+// slot; v heads copy to it.  Rows of q, k and v are q_stride, k_stride and
+// v_stride elements apart.  Order and math of transformer_layer.py:114-145
+// in one launch.
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
-    f16* __restrict__ q, f16* __restrict__ k, const f16* __restrict__ v,
+    const f16* q, int64_t q_stride, f16* q_out, f16* k, int64_t k_stride, const f16* __restrict__ v,
+    int64_t v_stride,
     const f16* __restrict__ qw, const f16* __restrict__ kw, float eps,
     const f16* __restrict__ cos_c, const f16* __restrict__ sin_c, int64_t n_pos,
     f16* __restrict__ kc, f16* __restrict__ vc, const int32_t* __restrict__ bt, int64_t bt_rows,
@@ -161,7 +165,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   if (hd >= hq + hkv) {  // v head: bit-exact copy of 256 bytes
     const int h = hd - hq - hkv;
     if (slot >= 0) {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(v + (r * hkv + h) * D);
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(v + r * v_stride + (int64_t)h * D);
       uint32_t* dst = reinterpret_cast<uint32_t*>(vc + slot + (int64_t)h * BS * D);
       dst[lane] = src[lane];
     }
@@ -173,9 +177,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   }
   const bool isk = hd >= hq;
   const int h = isk ? hd - hq : hd;
-  f16* x = isk ? k + (r * hkv + h) * D : q + (r * hq + h) * D;
+  const f16* xin = isk ? k + r * k_stride + (int64_t)h * D : q + r * q_stride + (int64_t)h * D;
+  f16* x = isk ? k + r * k_stride + (int64_t)h * D : q_out + (r * hq + h) * D;
   const f16* w = isk ? kw : qw;
-  float x0 = (float)x[lane], x1 = (float)x[lane + 64];
+  float x0 = (float)xin[lane], x1 = (float)xin[lane + 64];
   if (w != nullptr) {
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float rstd = 1.f / sqrtf(ss / (float)D + eps);
@@ -292,6 +297,40 @@ extern "C" int nsd_store_kvcache_prefill(const void* k, const void* v, void* k_c
   return launch_status("store_kvcache_prefill");
 }
 
+static int qk_norm_rope_store_impl(const void* q, int64_t q_stride, void* q_out, void* k, int64_t k_stride,
+                                   const void* v, int64_t v_stride, const void* q_norm_w, const void* k_norm_w,
+                                   float eps, const void* cos_cache, const void* sin_cache, int64_t n_positions,
+                                   void* k_cache, void* v_cache, const int32_t* block_table, int64_t bt_rows,
+                                   int64_t bt_stride, const int32_t* seq_ids, const int32_t* seq_lens,
+                                   int64_t n_rows, int64_t num_blocks, int num_layers, int layer,
+                                   int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int32_t* status, void* stream) {
+  int rc = check_cache_shape(num_layers, layer, num_kv_heads, head_dim, block_size, num_blocks,
+                             "qk_norm_rope_store");
+  if (rc) return rc;
+  if (num_q_heads <= 0 || n_rows < 0 || n_positions <= 0 || bt_rows <= 0 || bt_stride <= 0)
+    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: bad sizes");
+  if (n_rows == 0) return NSD_OK;
+  if (!q || !q_out || !k || !v || !cos_cache || !sin_cache || !k_cache || !v_cache || !block_table ||
+      !seq_ids || !seq_lens)
+    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: null pointer");
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: pass both norm weights or neither");
+  if (q_stride < (int64_t)num_q_heads * D || k_stride < (int64_t)num_kv_heads * D ||
+      v_stride < (int64_t)num_kv_heads * D || (q_stride | k_stride | v_stride) & 1)
+    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: row strides must be even and cover the heads");
+  const int64_t waves = n_rows * (num_q_heads + 2 * num_kv_heads);
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     as_stream(stream), static_cast<const f16*>(q), q_stride, static_cast<f16*>(q_out),
+                     static_cast<f16*>(k), k_stride, static_cast<const f16*>(v), v_stride,
+                     static_cast<const f16*>(q_norm_w), static_cast<const f16*>(k_norm_w), eps,
+                     static_cast<const f16*>(cos_cache), static_cast<const f16*>(sin_cache), n_positions,
+                     static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), block_table, bt_rows, bt_stride,
+                     seq_ids, seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads, num_kv_heads,
+                     status);
+  return launch_status("qk_norm_rope_store");
+}
+
 extern "C" int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const void* q_norm_w,
                                       const void* k_norm_w, float eps, const void* cos_cache,
                                       const void* sin_cache, int64_t n_positions, void* k_cache,
@@ -301,25 +340,25 @@ extern "C" int nsd_qk_norm_rope_store(void* q, void* k, const void* v, const voi
                                       int num_layers, int layer, int num_q_heads, int num_kv_heads,
                                       int head_dim, int block_size, int32_t* status,
                                       void* stream) {
-  int rc = check_cache_shape(num_layers, layer, num_kv_heads, head_dim, block_size, num_blocks,
-                             "qk_norm_rope_store");
-  if (rc) return rc;
-  if (num_q_heads <= 0 || n_rows < 0 || n_positions <= 0 || bt_rows <= 0 || bt_stride <= 0)
-    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: bad sizes");
-  if (n_rows == 0) return NSD_OK;
-  if (!q || !k || !v || !cos_cache || !sin_cache || !k_cache || !v_cache || !block_table ||
-      !seq_ids || !seq_lens)
-    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: null pointer");
-  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
-    return fail(NSD_ERR_INVALID, "qk_norm_rope_store: pass both norm weights or neither");
-  const int64_t waves = n_rows * (num_q_heads + 2 * num_kv_heads);
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
-                     as_stream(stream), static_cast<f16*>(q), static_cast<f16*>(k),
-                     static_cast<const f16*>(v), static_cast<const f16*>(q_norm_w),
-                     static_cast<const f16*>(k_norm_w), eps, static_cast<const f16*>(cos_cache),
-                     static_cast<const f16*>(sin_cache), n_positions, static_cast<f16*>(k_cache),
-                     static_cast<f16*>(v_cache), block_table, bt_rows, bt_stride, seq_ids,
-                     seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads, num_kv_heads,
-                     status);
-  return launch_status("qk_norm_rope_store");
+  return qk_norm_rope_store_impl(q, (int64_t)num_q_heads * D, q, k, (int64_t)num_kv_heads * D, v,
+                                 (int64_t)num_kv_heads * D, q_norm_w, k_norm_w, eps, cos_cache, sin_cache,
+                                 n_positions, k_cache, v_cache, block_table, bt_rows, bt_stride, seq_ids, seq_lens,
+                                 n_rows, num_blocks, num_layers, layer, num_q_heads, num_kv_heads, head_dim,
+                                 block_size, status, stream);
+}
+
+extern "C" int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_out, void* k,
+                                              int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                              const void* q_norm_w, const void* k_norm_w, float eps,
+                                              const void* cos_cache, const void* sin_cache,
+                                              int64_t n_positions, void* k_cache, void* v_cache,
+                                              const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
+                                              const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                                              int64_t num_blocks, int num_layers, int layer, int num_q_heads,
+                                              int num_kv_heads, int head_dim, int block_size, int32_t* status,
+                                              void* stream) {
+  return qk_norm_rope_store_impl(q, q_row_stride, q_out, k, k_row_stride, v, v_row_stride, q_norm_w, k_norm_w, eps,
+                                 cos_cache, sin_cache, n_positions, k_cache, v_cache, block_table, bt_rows,
+                                 bt_stride, seq_ids, seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads,
+                                 num_kv_heads, head_dim, block_size, status, stream);
 }

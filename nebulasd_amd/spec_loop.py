@@ -14,7 +14,8 @@ this package's gfx950 kernels:
 * the rest of the layer in the reference's order
   (transformer_layer.py:83-201, model.py:266-301): the residual buffer with
   ``fused_add_rmsnorm_inplace`` before attention and before the FFN, the
-  stacked up/gate GEMM with ``silu_and_mul_inplace``, and the post-layer's
+  stacked up/gate GEMM with ``silu_and_mul_inplace``, one fused q/k/v GEMM
+  (the reference runs three) whose row slices the prologue reads, and the post-layer's
   last-token norm with the fused lm_head + argmax (``post_layer_forward``);
   the GEMMs are library GEMMs through ``F.linear`` as in the reference
   (kernels/linear.py:3-12).  Weights are random (no checkpoints are
@@ -73,7 +74,7 @@ class RandomQwen3:
         self.layers = []
         for _ in range(mc.num_layers):
             self.layers.append(dict(
-                wq=w(hq * d, H), wk=w(hkv * d, H), wv=w(hkv * d, H), wo=w(H, hq * d),
+                wqkv=w((hq + 2 * hkv) * d, H), wo=w(H, hq * d),  # q, k, v projections stacked
                 wug=w(2 * I, H), wd=w(H, I),  # up rows first, then gate (weight.py:151)
                 n_in=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
                 n_post=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
@@ -108,9 +109,10 @@ class RandomQwen3:
         res = torch.zeros_like(x)
         for li, lw in enumerate(self.layers):
             fused_add_rmsnorm_inplace(x, res, lw["n_in"], eps)
-            q = F.linear(x, lw["wq"]).view(-1, hq, d)
-            k = F.linear(x, lw["wk"]).view(-1, hkv, d)
-            v = F.linear(x, lw["wv"]).view(-1, hkv, d)
+            qkv = F.linear(x, lw["wqkv"])  # one GEMM for the reference's three (transformer_layer.py:107-109)
+            q = qkv[:, :hq * d].view(-1, hq, d)
+            k = qkv[:, hq * d:(hq + hkv) * d].view(-1, hkv, d)
+            v = qkv[:, (hq + hkv) * d:].view(-1, hkv, d)
             o = attention(li, lw, q, k, v)
             o = F.linear(o.view(x.shape[0], -1), lw["wo"])
             fused_add_rmsnorm_inplace(o, res, lw["n_post"], eps)
@@ -128,6 +130,7 @@ class RandomQwen3:
         d = mc.head_dim
 
         def attention(li, lw, q, k, v):
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
             rmsnorm_inplace(q.view(-1, d), lw["q_norm"], mc.rms_norm_eps)
             rmsnorm_inplace(k.view(-1, d), lw["k_norm"], mc.rms_norm_eps)
             rotary_embedding_inplace(q, k, st)
@@ -144,9 +147,10 @@ class RandomQwen3:
         st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
         hq = mc.num_q_heads
 
-        def attention(li, lw, q, k, v):
-            qk_norm_rope_store(q, k, v, self.k_cache, self.v_cache, self.block_table,
-                               lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin)
+        def attention(li, lw, q_rows, k, v):
+            q = torch.empty(q_rows.shape, dtype=q_rows.dtype, device=dev)  # the prologue's contiguous q
+            qk_norm_rope_store(q_rows, k, v, self.k_cache, self.v_cache, self.block_table,
+                               lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin, q_out=q)
             o = torch.empty_like(q)
             if self.check is not None and self.check[0] == li:
                 lse = torch.empty((q.shape[0], hq), dtype=torch.float32, device=dev)

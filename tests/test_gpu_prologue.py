@@ -176,6 +176,41 @@ def test_fused_prologue_matches_oracle(gpu, name, model):
     assert torch.equal(w.v_cache, want_v)
 
 
+@pytest.mark.parametrize("name,model", [("draft_decode", QWEN3_0_6B), ("target_verify", QWEN3_8B)])
+def test_strided_prologue_equals_contiguous(gpu, name, model):
+    """q/k/v as row-strided slices of one fused projection output: the q
+    written to q_out, the rotated k (in place) and both cache pools are
+    bit-identical to the contiguous entry point's on copies; q is untouched."""
+    w = make_workload(name, 3, device=gpu)
+    mc, ec = ModelConfig(model), EngineConfig()
+    st, _, _ = _state(w, mc, gpu)
+    cos_c, sin_c = rope_cache(128, mc.rope_theta, 40960, gpu)
+    g = torch.Generator(device=gpu).manual_seed(6)
+    hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, 128
+    qkv = torch.randn((w.rows, (hq + 2 * hkv) * d), device=gpu, generator=g).half()
+    q = qkv[:, :hq * d].view(w.rows, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(w.rows, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(w.rows, hkv, d)
+    qc, kc_, vc_ = q.contiguous(), k.contiguous(), v.contiguous()
+    q_in = q.clone()
+    qw = (torch.rand(d, device=gpu, generator=g) + 0.5).half()
+    kw = (torch.rand(d, device=gpu, generator=g) + 0.5).half()
+    layer = 1
+    kpool, vpool = w.k_cache.clone(), w.v_cache.clone()
+    qk_norm_rope_store(qc, kc_, vc_, kpool, vpool, w.block_table, qw, kw, mc, ec, st, layer, cos_c, sin_c,
+                       validate=True)
+    q_out = torch.empty_like(qc)
+    qk_norm_rope_store(q, k, v, w.k_cache, w.v_cache, w.block_table, qw, kw, mc, ec, st, layer, cos_c, sin_c,
+                       validate=True, q_out=q_out)
+    torch.cuda.synchronize()
+    assert torch.equal(q_out, qc)
+    assert torch.equal(k, kc_)
+    assert torch.equal(q, q_in)
+    assert torch.equal(w.k_cache, kpool) and torch.equal(w.v_cache, vpool)
+    with pytest.raises(ValueError, match="q_out"):
+        qk_norm_rope_store(q, k, v, w.k_cache, w.v_cache, w.block_table, qw, kw, mc, ec, st, layer, cos_c, sin_c)
+
+
 def test_fused_equals_unfused(gpu):
     """One launch gives the result of rmsnorm -> rmsnorm -> rope -> store (to fp16 rounding),
     and each path's cache slots hold exactly the k/v that path produced."""
