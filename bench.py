@@ -581,12 +581,13 @@ def measure_layer_step(seed: int, reps: int = 20):
             torch.mm(x, lw["wq"].t(), out=q.view(T, -1))
             torch.mm(x, lw["wk"].t(), out=k.view(T, -1))
             torch.mm(x, lw["wv"].t(), out=v.view(T, -1))
-        if rest and fused_qkv:
-            qk_norm_rope_store(qs, ks, vs, w.k_cache, w.v_cache, w.block_table, lw["qn"], lw["kn"], mc, ec, st,
-                               kv_layer[i], cos, sin, q_out=q)
-        elif rest:
-            qk_norm_rope_store(q, k, v, w.k_cache, w.v_cache, w.block_table, lw["qn"], lw["kn"], mc, ec, st,
-                               kv_layer[i], cos, sin)
+        if rest:
+            if fused_qkv:
+                qk_norm_rope_store(qs, ks, vs, w.k_cache, w.v_cache, w.block_table, lw["qn"], lw["kn"], mc, ec,
+                                   st, kv_layer[i], cos, sin, q_out=q)
+            else:
+                qk_norm_rope_store(q, k, v, w.k_cache, w.v_cache, w.block_table, lw["qn"], lw["kn"], mc, ec, st,
+                                   kv_layer[i], cos, sin)
             paged_attention(q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, kv_layer[i], o)
         if gemms:
             torch.mm(o.view(T, -1), lw["wo"].t(), out=oo)
@@ -632,7 +633,7 @@ def measure_layer_step(seed: int, reps: int = 20):
         res.zero_()
 
     def snapshot():
-        return torch.cat([x.flatten(), res.flatten(), q.flatten()]).clone()
+        return torch.cat([x.flatten(), res.flatten(), q.flatten(), o.flatten()]).clone()
     for name, kw in (("layer", {}), ("layer_three_qkv_gemms", {"fused_qkv": False})):
         def one_pass(kw=kw):
             for i in range(n_layers):
