@@ -525,7 +525,7 @@ def measure_layer_step(seed: int, reps: int = 20):
     down GEMM.  Passes of four layers (weights of four distinct layers,
     1.7 GB, so each layer reads its weights from HBM): the whole layer, the
     GEMMs alone and the rest alone.  Floor: weight bytes + the attention's
-    K/V bytes at the device-copy rate.  Timed eagerly (see below).""" 
+    K/V bytes at the device-copy rate.  Timed eagerly (see below)."""
     import numpy as np
     import torch
     import torch.nn.functional as F
@@ -600,8 +600,8 @@ def measure_layer_step(seed: int, reps: int = 20):
         if gemms:
             torch.mm(ug[:, :I], lw["wd"].t(), out=x)
 
-    # Eager, not a graph: the library GEMMs may record memset nodes, which a
-    # captured graph must not hold.  `reps` passes of four layers are enqueued
+    # Eager, not a graph: captured with the library GEMMs these passes did not
+    # replay to the eager result, so they stay out of graphs.  `reps` passes of four layers are enqueued
     # back to back between two events; the host's enqueue time is kept too,
     # so a host-bound figure shows as host_us >= device us.
     stream = torch.cuda.current_stream()
@@ -622,56 +622,6 @@ def measure_layer_step(seed: int, reps: int = 20):
         host[name] = (time.perf_counter() - t0) * 1e6 / (reps * n_layers)
         e1.synchronize()
         out[name] = e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
-    # Device time from a HIP graph of the same passes, used only if every replay
-    # (with eager work and synchronisations between them) reproduces the eager
-    # result from the same starting state: the library GEMMs must not record
-    # anything a replay gets wrong.
-    graph = {}
-
-    def reset():
-        x.copy_(x0)
-        res.zero_()
-
-    def snapshot():
-        return torch.cat([x.flatten(), res.flatten(), q.flatten(), o.flatten()]).clone()
-    for name, kw in (("layer", {}), ("layer_three_qkv_gemms", {"fused_qkv": False})):
-        def one_pass(kw=kw):
-            for i in range(n_layers):
-                layer(i, **kw)
-        reset()
-        one_pass()
-        torch.cuda.synchronize()
-        want = snapshot()
-        gstream = torch.cuda.Stream()
-        with torch.cuda.stream(gstream):
-            reset()
-            gstream.synchronize()
-            one_pass()  # warm-up on the capture stream
-            gstream.synchronize()
-            cg = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(cg, stream=gstream):
-                one_pass()
-        ok = True
-        for _ in range(3):
-            reset()
-            torch.cuda.synchronize()
-            cg.replay()
-            torch.cuda.synchronize()
-            ok &= bool(torch.equal(snapshot(), want))
-            torch.mm(x0[:8], layers[0]["wo"][:64, :H].t())  # eager work between replays
-        if ok:
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            with torch.cuda.stream(gstream):
-                cg.replay()
-                ev[0].record(gstream)
-                for _ in range(reps):
-                    cg.replay()
-                ev[1].record(gstream)
-            ev[1].synchronize()
-            graph[name] = ev[0].elapsed_time(ev[1]) * 1e3 / (reps * n_layers)
-        else:
-            graph[name] = None
-        del cg
     kv_bytes = w.algorithmic_bytes()
     copy = getattr(measure_layer_step, "copy_gbps", None)
     floor = (weight_bytes + (kv_bytes or 0)) / (copy * 1e3) if copy and kv_bytes else None
@@ -680,8 +630,6 @@ def measure_layer_step(seed: int, reps: int = 20):
     return {"workload": "layer_step_target_verify", "kind": "whole_layer", "rows": T,
             "us_per_layer": out["layer"], "gemms_only_us": out["gemms_only"], "rest_only_us": out["rest_only"],
             "us_per_layer_three_qkv_gemms": out["layer_three_qkv_gemms"],
-            "graph_us_per_layer": graph.get("layer"),
-            "graph_us_per_layer_three_qkv_gemms": graph.get("layer_three_qkv_gemms"),
             "host_enqueue_us_per_layer": host,
             "weight_bytes_per_layer": weight_bytes, "kv_bytes_per_layer": kv_bytes,
             "floor_us_at_copy_rate": floor,
@@ -995,14 +943,10 @@ def main():
     if args.layer_step:
         measure_layer_step.copy_gbps = copy_gbps
         r2 = measure_layer_step(args.seed)
-        print("# target verify layer: %.1f us eager, graph %s us (three q/k/v GEMMs %.1f eager, graph %s; GEMMs alone "
-              "%.1f, rest alone %.1f; floor %s us)" % (
-            r2["us_per_layer"], "%.1f" % r2["graph_us_per_layer"] if r2["graph_us_per_layer"] else "n/a",
-            r2["us_per_layer_three_qkv_gemms"],
-            "%.1f" % r2["graph_us_per_layer_three_qkv_gemms"] if r2["graph_us_per_layer_three_qkv_gemms"] else "n/a",
-            r2["gemms_only_us"], r2["rest_only_us"],
-            "%.1f" % r2["floor_us_at_copy_rate"] if r2["floor_us_at_copy_rate"] else "n/a"),
-            file=sys.stderr, flush=True)
+        print("# target verify layer: %.1f us (three q/k/v GEMMs %.1f; GEMMs alone %.1f, rest alone %.1f; floor %s us)"
+              % (r2["us_per_layer"], r2["us_per_layer_three_qkv_gemms"], r2["gemms_only_us"], r2["rest_only_us"],
+                 "%.1f" % r2["floor_us_at_copy_rate"] if r2["floor_us_at_copy_rate"] else "n/a"),
+              file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.layer_rest:
         r2 = measure_layer_rest(args.seed, cpu_seconds=args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
