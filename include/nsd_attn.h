@@ -203,6 +203,29 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
                         int32_t* status, void* stream);
 
 /*
+ * nsd_paged_attention_noalloc: nsd_paged_attention without a workspace
+ * argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * has no counterpart in the reference, whose wrapper allocates its partials
+ * per call (swiftLLM/swiftllm/worker/kernels/paged_attn.py:170-180).
+ * The partials and arrival counters live in a static device array of
+ * NSD_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); a plan
+ * that needs more partial bytes than it holds (less 256 KiB of counters), or
+ * more than 65,536 counters, is rejected with NSD_ERR_WORKSPACE.  The call
+ * allocates nothing.  Its first call on a device clears the counters with a
+ * fill kernel on `stream`.  Every call on one GPU shares the array: calls
+ * that overlap on one GPU (two streams, two threads) race and must not
+ * overlap.  Same arguments, results and errors as nsd_paged_attention.
+ */
+#define NSD_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int nsd_paged_attention_noalloc(const void* q, void* o, float* lse, const void* k_cache,
+                                const void* v_cache, int64_t num_blocks, int num_layers, int layer,
+                                int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                const int32_t* block_table, int64_t bt_stride,
+                                const int32_t* plan_host, const int32_t* plan_dev,
+                                float softmax_scale, int32_t* status, void* stream);
+
+/*
  * Prefill (prompt) attention, causal within each prompt of a packed batch.
  * Replaces flash_attn_varlen_func
  * (swiftLLM/swiftllm/worker/layers/transformer_layer.py:7-32, called at

@@ -41,6 +41,7 @@
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB
 //   contiguous at ((blk*L + layer)*Hkv + head)*16*128 (:49-50, :70-71).
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -641,13 +642,31 @@ extern "C" int nsd_attn_num_workers(int max_rows, int* n_workers) {
   return NSD_OK;
 }
 
-extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
-                                   const void* v_cache, int64_t num_blocks, int num_layers,
-                                   int layer, int num_q_heads, int num_kv_heads, int head_dim,
-                                   int block_size, const int32_t* block_table, int64_t bt_stride,
-                                   const int32_t* plan_host, const int32_t* plan_dev,
-                                   void* workspace, int64_t workspace_bytes, float softmax_scale,
-                                   int32_t* status, void* stream) {
+// Scratch of nsd_paged_attention_noalloc: one copy of this array per GPU the
+// library runs on, held until the process ends.  Arrival counters sit at its
+// start (a fixed place, so every call finds them at zero: each launch leaves
+// the counters it used at zero), the partials after them.
+static __device__ __align__(256) char scratch[NSD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Bytes of the fp32 partials a plan needs: normalised O and log2-sum-exp
+// per partial slot, rounded up to 256 bytes.
+int64_t plan_partial_bytes(const int32_t* plan_host) {
+  return ((int64_t)plan_host[kPlanSlots] * plan_host[kPlanRowsMax] * (int64_t)(D + 1) * 4 + 255) /
+         256 * 256;
+}
+
+// Shared body of the two attention entry points: `part` holds the partials
+// (`part_capacity` bytes) and `counters` the arrival counters
+// (`counter_capacity` of them, zero between calls).
+int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache,
+                         const void* v_cache, int64_t num_blocks, int num_layers, int layer,
+                         int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                         const int32_t* block_table, int64_t bt_stride, const int32_t* plan_host,
+                         const int32_t* plan_dev, void* part, int64_t part_capacity,
+                         int32_t* counters, int64_t counter_capacity, float softmax_scale,
+                         int32_t* status, void* stream) {
   if (head_dim != D) return fail(NSD_ERR_UNSUPPORTED, "paged_attention: head_dim=%d (only 128)", head_dim);
   if (block_size != BS)
     return fail(NSD_ERR_UNSUPPORTED, "paged_attention: block_size=%d (only 16)", block_size);
@@ -704,11 +723,14 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
         return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (piece %d)", i);
     }
   }
-  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(D + 1) * 4 + 255) / 256 * 256;
-  const int64_t need = n_combine > 0 ? part_bytes + n_combine * 4 : 0;
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
-    return fail(NSD_ERR_WORKSPACE, "paged_attention: workspace %lld bytes < %lld needed",
-                (long long)workspace_bytes, (long long)need);
+  const int64_t part_bytes = plan_partial_bytes(plan_host);
+  if (n_combine > 0 && (part == nullptr || part_capacity < part_bytes || !aligned16(part) ||
+                        counters == nullptr || counter_capacity < n_combine))
+    return fail(NSD_ERR_WORKSPACE,
+                "paged_attention: workspace holds %lld partial bytes and %lld counters, the plan "
+                "needs %lld and %d",
+                (long long)part_capacity, (long long)counter_capacity, (long long)part_bytes,
+                n_combine);
 
   AttnArgs args;
   args.q = static_cast<const f16*>(q);
@@ -720,9 +742,9 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
   args.bt_stride = bt_stride;
   args.workers = plan_dev + plan_host[kPlanOffWorkers];
   args.pieces = plan_dev + plan_host[kPlanOffPieces];
-  args.part_o = static_cast<float*>(workspace);
-  args.part_lse = static_cast<float*>(workspace) + n_slots * rows_max * D;
-  args.counters = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + part_bytes);
+  args.part_o = static_cast<float*>(part);
+  args.part_lse = static_cast<float*>(part) + n_slots * rows_max * D;
+  args.counters = counters;
   args.status = status;
   args.num_blocks = num_blocks;
   args.blk_stride = (int64_t)num_layers * num_kv_heads * BS * D;
@@ -742,4 +764,99 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
     case 3: return launch_nt<3>(args, grid, st);
     default: return launch_nt<4>(args, grid, st);
   }
+}
+
+constexpr int64_t kScratchCounterBytes = 256 * 1024;
+constexpr int64_t kScratchBytes = int64_t(NSD_NOALLOC_SCRATCH_BYTES);
+static_assert(kScratchBytes > kScratchCounterBytes, "scratch layout");
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch_ptr[kMaxScratchDevices] = {};  // device address of `scratch`, per device
+
+__global__ void zero_words_kernel(int32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+// Device address of the current device's scratch.  On the first call on a
+// device it is looked up (the array's host-side name is not a device
+// address) and its counter region cleared by a fill kernel on `stream`.
+int scratch_for_current_device(hipStream_t stream, char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NSD_ERR_HIP, "paged_attention_noalloc: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(NSD_ERR_UNSUPPORTED, "paged_attention_noalloc: device %d >= %d", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(NSD_ERR_HIP, "paged_attention_noalloc: scratch address: %s",
+                  hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, stream,
+                       static_cast<int32_t*>(ptr), kScratchCounterBytes / 4);
+    const int rc = launch_status("paged_attention_noalloc: scratch clear");
+    if (rc != NSD_OK) return rc;
+    g_scratch_ptr[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return NSD_OK;
+}
+
+}  // namespace
+
+extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
+                                   const void* v_cache, int64_t num_blocks, int num_layers,
+                                   int layer, int num_q_heads, int num_kv_heads, int head_dim,
+                                   int block_size, const int32_t* block_table, int64_t bt_stride,
+                                   const int32_t* plan_host, const int32_t* plan_dev,
+                                   void* workspace, int64_t workspace_bytes, float softmax_scale,
+                                   int32_t* status, void* stream) {
+  if (!plan_host) return fail(NSD_ERR_INVALID, "paged_attention: null plan");
+  // workspace: partials, then the arrival counters
+  const int64_t part_bytes = plan_partial_bytes(plan_host);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t counters = workspace_bytes > part_bytes ? (workspace_bytes - part_bytes) / 4 : 0;
+  return paged_attention_impl(q, o, lse, k_cache, v_cache, num_blocks, num_layers, layer,
+                              num_q_heads, num_kv_heads, head_dim, block_size, block_table,
+                              bt_stride, plan_host, plan_dev, ws, workspace_bytes,
+                              ws ? reinterpret_cast<int32_t*>(ws + part_bytes) : nullptr,
+                              counters, softmax_scale, status, stream);
+}
+
+extern "C" int nsd_paged_attention_noalloc(const void* q, void* o, float* lse,
+                                           const void* k_cache, const void* v_cache,
+                                           int64_t num_blocks, int num_layers, int layer,
+                                           int num_q_heads, int num_kv_heads, int head_dim,
+                                           int block_size, const int32_t* block_table,
+                                           int64_t bt_stride, const int32_t* plan_host,
+                                           const int32_t* plan_dev, float softmax_scale,
+                                           int32_t* status, void* stream) {
+  if (!plan_host) return fail(NSD_ERR_INVALID, "paged_attention_noalloc: null plan");
+  if (plan_host[kPlanMagic] != kPlanMagicValue || plan_host[kPlanVersion] != kPlanVersionValue)
+    return fail(NSD_ERR_INVALID, "paged_attention_noalloc: not a plan (bad magic/version)");
+  const int64_t part_bytes = plan_partial_bytes(plan_host);
+  const int64_t n_combine = plan_host[kPlanCombines];
+  if (part_bytes > kScratchBytes - kScratchCounterBytes || n_combine * 4 > kScratchCounterBytes)
+    return fail(NSD_ERR_WORKSPACE,
+                "paged_attention_noalloc: the plan needs %lld partial bytes and %lld counters; "
+                "the static scratch holds %lld and %lld (use nsd_paged_attention with a "
+                "workspace)",
+                (long long)part_bytes, (long long)n_combine,
+                (long long)(kScratchBytes - kScratchCounterBytes),
+                (long long)(kScratchCounterBytes / 4));
+  hipStream_t st = as_stream(stream);
+  char* base = nullptr;
+  const int rc = scratch_for_current_device(st, &base);
+  if (rc != NSD_OK) return rc;
+  return paged_attention_impl(q, o, lse, k_cache, v_cache, num_blocks, num_layers, layer,
+                              num_q_heads, num_kv_heads, head_dim, block_size, block_table,
+                              bt_stride, plan_host, plan_dev, base + kScratchCounterBytes,
+                              kScratchBytes - kScratchCounterBytes,
+                              reinterpret_cast<int32_t*>(base), kScratchCounterBytes / 4,
+                              softmax_scale, status, stream);
 }

@@ -345,3 +345,28 @@ def test_attention_rejects_corrupt_plans(lib):
         rc = _attention_with_plan(lib, w)
         assert rc == 1, (where, rc, _lib.last_error())
         assert "corrupt plan" in _lib.last_error() and where in _lib.last_error()
+
+
+def test_noalloc_rejects_plans_larger_than_its_scratch(lib):
+    """A plan whose partials exceed the allocation-free entry point's static
+    scratch is refused before any HIP call, with the sizes in the message."""
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import plan_words
+
+    # 32 requests x 16 verify rows (64 query rows per kv head) over 32k contexts
+    # cut across 2048 workers: thousands of 64-row partial slots (> 16 MiB)
+    sids = [r for r in range(32) for _ in range(16)]
+    slens = [32000 + i + 1 for _ in range(32) for i in range(16)]
+    words, _ = plan_words(sids, slens, 32, 8, 128, 16, 32, 2100, 2048)
+    slots, rows_max = int(words[_lib.PLAN_SLOTS]), int(words[_lib.PLAN_ROWS_MAX])
+    assert slots * rows_max * 129 * 4 > (16 << 20), "the plan should not fit the scratch"
+    rc = lib.nsd_paged_attention_noalloc(
+        None, None, None, None, None, 24576, 36, 0, 32, 8, 128, 16, None, 2100,
+        words.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, 0.088, None, None)
+    assert rc == _lib.NSD_ERR_WORKSPACE and "static scratch" in _lib.last_error()
+    # not a plan: rejected as such
+    bad = np.zeros(_lib.PLAN_HEADER_WORDS, np.int32)
+    rc = lib.nsd_paged_attention_noalloc(
+        None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
+        bad.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, 0.088, None, None)
+    assert rc == 1 and "not a plan" in _lib.last_error()
