@@ -153,13 +153,12 @@ int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_
  *     max_group_rows = 1 keeps every row its own group;
  *   - the (group, kv head, 16-token block) stream is cut into n_workers
  *     contiguous ranges of near-equal cost (blocks plus a fixed charge per
- *     range piece), one per workgroup, whose waves claim the range's blocks
- *     a few at a time; a (group, kv head) segment cut across ranges gets
- *     fp32 partials (normalised O and log2-sum-exp), merged inside the same
- *     launch by the workgroup that writes the segment's last partial.
+ *     range piece), one per workgroup; a (group, kv head) segment cut
+ *     across ranges gets fp32 partials (normalised O and log2-sum-exp),
+ *     merged in slot order by a second launch of the same call.
  * nsd_attn_plan_bound gives the plan size in int32 words for plans that fit
- * n_workers workers.  A plan may use more workers than asked (each worker
- * holds at most 32 pieces); when it does not fit `plan_capacity`,
+ * n_workers workers.  A plan may use more workers than asked (a worker
+ * streams at most 4 pieces and 1024 blocks); when it does not fit `plan_capacity`,
  * nsd_attn_plan_build returns NSD_ERR_WORKSPACE and sets *plan_words to the
  * size needed, so the caller can retry.
  * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
@@ -189,15 +188,17 @@ int nsd_attn_num_workers(int max_rows, int* n_workers);
  * softmax-weighted sum of V (fp16 out, fp32 math).  If lse != NULL it also
  * writes ln(sum exp(score)) as fp32 [n_rows, Hq].
  * plan_host / plan_dev: the same plan words on the host and on the device.
- * workspace: device buffer of at least the bytes reported by the plan, 16-byte
- * aligned and ZERO-FILLED before its first use: its tail holds one arrival
- * counter per split segment, which every call leaves at zero again.  Calls
+ * workspace: device buffer of at least the bytes reported by the plan (the
+ * partials of the segments cut across workgroups), 16-byte aligned.  Calls
  * that share a workspace must be ordered on one stream (never concurrent).
+ * bt_rows / bt_stride: the block table's shape; the plan must have been
+ * built for this row stride and at most this many rows.
+ * Results are bit-reproducible: identical inputs give identical o and lse.
  */
 int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
                         const void* v_cache, int64_t num_blocks, int num_layers, int layer,
                         int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                        const int32_t* block_table, int64_t bt_stride,
+                        const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
                         const int32_t* plan_host, const int32_t* plan_dev,
                         void* workspace, int64_t workspace_bytes, float softmax_scale,
                         int32_t* status, void* stream);
@@ -208,22 +209,21 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
  * has no counterpart in the reference, whose wrapper allocates its partials
  * per call (swiftLLM/swiftllm/worker/kernels/paged_attn.py:170-180).
- * The partials and arrival counters live in a static device array of
- * NSD_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); a plan
- * that needs more partial bytes than it holds (less 256 KiB of counters), or
- * more than 65,536 counters, is rejected with NSD_ERR_WORKSPACE.  The call
- * allocates nothing.  Its first call on a device clears the counters with a
- * fill kernel on `stream`.  Every call on one GPU shares the array: calls
- * that overlap on one GPU (two streams, two threads) race and must not
- * overlap.  Same arguments, results and errors as nsd_paged_attention.
+ * The partials live in a static device array of NSD_NOALLOC_SCRATCH_BYTES
+ * per GPU (held until the process ends); a plan that needs more partial
+ * bytes than it holds is rejected with NSD_ERR_WORKSPACE.  The call
+ * allocates nothing.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (two streams, two threads) race and must not overlap.
+ * Same arguments, results and errors as nsd_paged_attention.
  */
 #define NSD_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int nsd_paged_attention_noalloc(const void* q, void* o, float* lse, const void* k_cache,
                                 const void* v_cache, int64_t num_blocks, int num_layers, int layer,
                                 int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                const int32_t* block_table, int64_t bt_stride,
-                                const int32_t* plan_host, const int32_t* plan_dev,
-                                float softmax_scale, int32_t* status, void* stream);
+                                const int32_t* block_table, int64_t bt_rows,
+                                int64_t bt_stride, const int32_t* plan_host,
+                                const int32_t* plan_dev, float softmax_scale, int32_t* status,
+                                void* stream);
 
 /*
  * Prefill (prompt) attention, causal within each prompt of a packed batch.

@@ -28,7 +28,8 @@ COPY_ENGINE_KERNEL = 1
 # Plan header word indices (nsd_common.h, enum PlanHeader).
 PLAN_MAGIC, PLAN_VERSION, PLAN_ROWS, PLAN_GROUPS, PLAN_PIECES, PLAN_WORKERS, PLAN_COMBINES, \
     PLAN_SLOTS, PLAN_ROWS_MAX, PLAN_HQ, PLAN_HKV, PLAN_OFF_GROUPS, PLAN_OFF_WSTART, \
-    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_STRIDE, PLAN_RING_STAGES = range(18)
+    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_STRIDE, PLAN_BT_ROWS, \
+    PLAN_BT_STRIDE, PLAN_MAX_BLOCKS = range(20)
 
 _I32P = POINTER(c_int32)
 
@@ -61,12 +62,12 @@ SIGNATURES = {
     "nsd_attn_num_workers": (c_int, [c_int, POINTER(c_int)]),
     "nsd_paged_attention": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
-                c_int, c_int, c_int, c_void_p, c_int64, _I32P, c_void_p, c_void_p, c_int64,
-                c_float, c_void_p, c_void_p]),
+                c_int, c_int, c_int, c_void_p, c_int64, c_int64, _I32P, c_void_p, c_void_p,
+                c_int64, c_float, c_void_p, c_void_p]),
     "nsd_paged_attention_noalloc": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
-                c_int, c_int, c_int, c_void_p, c_int64, _I32P, c_void_p, c_float, c_void_p,
-                c_void_p]),
+                c_int, c_int, c_int, c_void_p, c_int64, c_int64, _I32P, c_void_p, c_float,
+                c_void_p, c_void_p]),
     "nsd_write_block_ranges": (
         c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                 c_void_p]),

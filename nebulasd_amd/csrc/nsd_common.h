@@ -31,15 +31,16 @@ enum PlanHeader {
   kPlanOffCombines,    // word offset of combines [n_combines][kPieceWords]
   kPlanWords,          // total words
   kPlanPieceStride,    // piece records per worker: worker w's records start at w * stride
-  kPlanRingStages,     // blocks per claimed group the records' group counts assume
+  kPlanBtRows,         // block-table rows every piece's seq_id was checked against
+  kPlanBtStride,       // block-table row length every piece's block range was checked against
+  kPlanMaxBlocks,      // most 16-token blocks one worker streams
 };
-static_assert(kPlanRingStages < NSD_PLAN_HEADER_WORDS, "plan header size");
+static_assert(kPlanMaxBlocks < NSD_PLAN_HEADER_WORDS, "plan header size");
 
 // A piece: blocks [blk_begin, blk_end) of one (group, kv head) segment, with
 // the group's description inlined so a worker needs one record per piece.
-// The workgroup's waves claim a piece's blocks in groups of ring_stages(nt)
-// consecutive blocks; kPieceGroupEnd counts the groups of the worker's pieces
-// up to and including this one.
+// kPieceKvBase counts the blocks of the worker's earlier pieces: the piece's
+// block ids sit at that offset of the worker's id list.
 enum PieceField {
   kPieceHead = 0,   // kv head
   kPieceBlkBegin,   // first 16-token block
@@ -52,7 +53,7 @@ enum PieceField {
   kPieceComb,       // combine record of the segment, or -1
   kPieceCombFirst,  // first partial slot of the segment
   kPieceCombSlots,  // partial slots of the segment
-  kPieceGroupEnd,   // groups of this worker's pieces 0 .. this one
+  kPieceKvBase,     // blocks of this worker's pieces before this one
   kPieceWords,
 };
 // A worker-table row: {first piece, end piece, <first piece record>, 0, 0}.
@@ -64,19 +65,12 @@ constexpr int kWorkerFirstPiece = 2;
 enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
 
 constexpr int32_t kPlanMagicValue = 0x4E534450;
-constexpr int32_t kPlanVersionValue = 6;
+constexpr int32_t kPlanVersionValue = 7;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
 constexpr int kMaxGroupRows = 64;
 constexpr int kMaxSlotsPerSegment = 128;
-constexpr int kMaxWorkerPieces = 32;   // pieces one workgroup keeps records of
-
-// Attention kernel shape for groups of up to 16*nt query rows (nt = 1..4):
-// K/V ring depth, which is also the size of a claimed group of blocks, and
-// waves per workgroup (one workgroup per compute unit).  Every shape now
-// streams with eight waves and a one-block ring; the plan still records the
-// depth it was built for, so a kernel built for another depth rejects it.
-constexpr int ring_stages(int /*nt*/) { return 1; }
-constexpr int attn_waves(int /*nt*/) { return 8; }
+constexpr int kMaxWorkerPieces = 4;    // pieces one workgroup streams (their query rows stay in registers)
+constexpr int kMaxWorkerBlocks = 1024; // blocks one workgroup streams (its LDS id list)
 
 }  // namespace nsd

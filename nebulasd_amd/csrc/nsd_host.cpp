@@ -14,13 +14,12 @@ namespace nsd {
 namespace {
 thread_local std::string g_last_error;
 // Cost model of the planner, in 16-token blocks of streaming: a piece costs
-// its blocks rounded up to whole claimed groups plus a fixed kPieceCostBlocks
-// for what ends it (the waves drain and merge, and a split segment's partial
-// is written and merged later); 24 was the fastest of 8..48 on the
-// verify and decode shapes.  A worker opens another piece only if at least
-// kMinPieceBlocks of its budget remain for it.
+// its blocks plus a fixed kPieceCostBlocks for what it adds to the stream
+// (the ring items that bring its query rows, the output or partial it
+// writes).  A worker opens another piece only if at least kMinPieceBlocks of
+// its budget remain for it.
 constexpr int64_t kMinPieceBlocks = 4;
-constexpr int64_t kPieceCostBlocks = 24;
+constexpr int64_t kPieceCostBlocks = 3;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -114,10 +113,8 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   // 3. contiguous block ranges per worker of near-equal cost (the cost model
   //    above).  The target cost is the smallest one that fits the stream into
   //    the workers; it also keeps every segment under kMaxSlotsPerSegment
-  //    pieces and every worker under kMaxWorkerPieces pieces.
-  const int nt = std::max(1, (rows_max + 15) / 16);
-  const int64_t stages = ring_stages(nt);
-  auto groups_of = [&](int64_t blocks) { return (blocks + stages - 1) / stages; };
+  //    pieces, every worker under kMaxWorkerPieces pieces and
+  //    kMaxWorkerBlocks blocks.
   int64_t max_seg = 0;
   for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
   const int64_t cmin = kPieceCostBlocks + std::max<int64_t>(
@@ -127,17 +124,18 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   auto cut_stream = [&](int64_t cap, std::vector<int64_t>* cuts) {
     int64_t used = 0, pos = 0, seg_i = 0;
     while (pos < total) {
-      int64_t budget = cap;
+      int64_t budget = cap, room = kMaxWorkerBlocks;
       int opened = 0;
       if (cuts) cuts->push_back(-1);  // worker marker
-      while (pos < total && opened < kMaxWorkerPieces) {
+      while (pos < total && opened < kMaxWorkerPieces && room > 0) {
         while (seg_start[seg_i + 1] <= pos) ++seg_i;
         if (opened > 0 && budget < kPieceCostBlocks + kMinPieceBlocks) break;
-        const int64_t take = std::max<int64_t>(
-            1, std::min(budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos));
+        const int64_t take = std::min(room, std::max<int64_t>(
+            1, std::min(budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos)));
         if (cuts) cuts->insert(cuts->end(), {pos, pos + take});
         pos += take;
-        budget -= kPieceCostBlocks + groups_of(take) * stages;
+        room -= take;
+        budget -= kPieceCostBlocks + take;
         ++opened;
         if (budget <= 0) break;
       }
@@ -146,7 +144,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
     return used;
   };
   const int64_t want = std::max<int64_t>(1, n_workers);
-  int64_t lo = cmin, hi = std::max(cmin, total + n_segs * (kPieceCostBlocks + stages));
+  int64_t lo = cmin, hi = std::max(cmin, total + n_segs * (kPieceCostBlocks + 1));
   if (total > 0 && cut_stream(lo, nullptr) > want) {
     while (lo + 1 < hi) {  // smallest cap that fits in `want` workers
       const int64_t mid = (lo + hi) / 2;
@@ -211,20 +209,21 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t n_combines = (int64_t)combines.size() / kPieceWords;
 
   // 5. records at a fixed stride per worker (zero records fill the gaps),
-  //    each with its worker's running group count; the worker table holds
-  //    each worker's record range and an inline copy of its first record.
-  int64_t stride = 0;
+  //    each with the blocks of its worker's earlier pieces; the worker table
+  //    holds each worker's record range and an inline copy of its first record.
+  int64_t stride = 0, max_blocks = 0;
   for (int64_t v = 0; v < grid; ++v) stride = std::max<int64_t>(stride, wstart[v + 1] - wstart[v]);
   std::vector<int32_t> records(kPieceWords * grid * stride, 0);
   std::vector<int32_t> wtable(kWorkerWords * grid, 0);
   for (int64_t v = 0; v < grid; ++v) {
-    int64_t groups_run = 0;
+    int64_t blocks_run = 0;
     for (int64_t i = wstart[v]; i < wstart[v + 1]; ++i) {
       int32_t* r = &records[kPieceWords * (v * stride + (i - wstart[v]))];
       std::copy(&pieces[kPieceWords * i], &pieces[kPieceWords * (i + 1)], r);
-      groups_run += groups_of(r[kPieceBlkEnd] - r[kPieceBlkBegin]);
-      r[kPieceGroupEnd] = (int32_t)groups_run;
+      r[kPieceKvBase] = (int32_t)blocks_run;
+      blocks_run += r[kPieceBlkEnd] - r[kPieceBlkBegin];
     }
+    max_blocks = std::max(max_blocks, blocks_run);
     int32_t* row = &wtable[kWorkerWords * v];
     row[0] = (int32_t)(v * stride);
     row[1] = (int32_t)(v * stride + wstart[v + 1] - wstart[v]);
@@ -266,15 +265,17 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   h[kPlanOffCombines] = (int32_t)off_combines;
   h[kPlanWords] = (int32_t)words;
   h[kPlanPieceStride] = (int32_t)stride;
-  h[kPlanRingStages] = (int32_t)stages;
+  h[kPlanBtRows] = (int32_t)std::min<int64_t>(bt_rows, INT32_MAX);
+  h[kPlanBtStride] = (int32_t)std::min<int64_t>(bt_stride, INT32_MAX);
+  h[kPlanMaxBlocks] = (int32_t)max_blocks;
   std::copy(groups.begin(), groups.end(), h + off_groups);
   std::copy(wtable.begin(), wtable.end(), h + off_wstart);
   std::copy(records.begin(), records.end(), h + off_pieces);
   std::copy(combines.begin(), combines.end(), h + off_combines);
 
   *plan_words = words;
-  // partial O and log-sum-exp per slot, then one arrival counter per combine
+  // partial O and log-sum-exp per slot
   const int64_t part_bytes = (n_slots * rows_max * (int64_t)(kHeadDim + 1) * 4 + 255) / 256 * 256;
-  *workspace_bytes = n_combines > 0 ? part_bytes + (n_combines * 4 + 255) / 256 * 256 : 0;
+  *workspace_bytes = n_combines > 0 ? part_bytes : 0;
   return NSD_OK;
 }

@@ -63,8 +63,8 @@ class LlamaInferState:
     def get_attn_plan(self, model_config, engine_config, block_table: torch.Tensor) -> AttnPlan:
         """The plan of this forward's decode rows (built on first use, reused by all layers)."""
         plan = self.attn_plan
-        if (plan is None or plan.num_q_heads != model_config.num_q_heads
-                or plan.num_kv_heads != model_config.num_kv_heads):
+        if plan is None or not plan.fits(model_config.num_q_heads, model_config.num_kv_heads,
+                                         block_table):
             sids, slens = self.decode_rows_host()
             plan = build_attn_plan(
                 sids, slens, model_config.num_q_heads, model_config.num_kv_heads,

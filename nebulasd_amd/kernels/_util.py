@@ -27,6 +27,18 @@ def require(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
+def check_block_table(block_table: torch.Tensor, engine_config) -> None:
+    """The block table's row length must be ``engine_config.max_blocks_per_seq``:
+    the reference kernels index rows with that stride (paged_attn.py:208,
+    kvcache_mgmt.py:121), these wrappers with ``block_table.shape[1]``."""
+    require(block_table, torch.int32, "block_table")
+    if block_table.dim() != 2:
+        raise ValueError("block_table must be [rows, max_blocks_per_seq]")
+    if int(engine_config.max_blocks_per_seq) != block_table.shape[1]:
+        raise ValueError(f"block_table rows hold {block_table.shape[1]} entries but "
+                         f"engine_config.max_blocks_per_seq is {engine_config.max_blocks_per_seq}")
+
+
 def cache_dims(k_cache: torch.Tensor):
     """(num_blocks, num_layers, num_kv_heads, block_size, head_dim) of a KV cache."""
     if k_cache.dim() != 5:

@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._util import StatusWord, cache_dims, ptr, require, require_cuda, stream_of
+from ._util import StatusWord, cache_dims, check_block_table, ptr, require, require_cuda, stream_of
 
 
 def store_kvcache(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -24,7 +24,7 @@ def store_kvcache(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cac
     require_cuda(k, v, k_cache, v_cache, block_table)
     for t, n in ((k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         require(t, torch.float16, n)
-    require(block_table, torch.int32, "block_table")
+    check_block_table(block_table, engine_config)
     require(infer_state.seq_ids, torch.int32, "infer_state.seq_ids")
     require(infer_state.decoding_seq_lens, torch.int32, "infer_state.decoding_seq_lens")
     n_blocks, n_layers, hkv, bs, d = cache_dims(k_cache)

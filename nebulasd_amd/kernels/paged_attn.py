@@ -11,7 +11,7 @@ import torch
 
 from .. import _lib
 from ..plan import plan_for
-from ._util import StatusWord, cache_dims, ptr, require, require_cuda, stream_of
+from ._util import StatusWord, cache_dims, check_block_table, ptr, require, require_cuda, stream_of
 
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -29,7 +29,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     require(q, torch.float16, "q")
     require(k_cache, torch.float16, "k_cache")
     require(v_cache, torch.float16, "v_cache")
-    require(block_table, torch.int32, "block_table")
+    check_block_table(block_table, engine_config)
     require(o, torch.float16, "o")
     if engine_config.block_size != k_cache.shape[3]:
         raise ValueError("engine_config.block_size does not match the cache layout")
@@ -47,11 +47,13 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     if rows == 0:
         return
     plan = plan_for(infer_state, model_config, engine_config, block_table)
+    if plan.n_rows != rows:
+        raise ValueError(f"the forward's attention plan covers {plan.n_rows} rows, q has {rows}")
     status = StatusWord(q.device) if validate else None
     _lib.call("nsd_paged_attention",
               q.data_ptr(), o.data_ptr(), ptr(lse), k_cache.data_ptr(), v_cache.data_ptr(),
               n_blocks, n_layers, int(cur_layer), hq, hkv, d, bs, block_table.data_ptr(),
-              block_table.shape[1], plan.host_ptr(), plan.dev.data_ptr(),
+              block_table.shape[0], block_table.shape[1], plan.host_ptr(), plan.dev.data_ptr(),
               plan.workspace.data_ptr(), plan.workspace.numel(),
               float(infer_state.softmax_scale), ptr(status.t) if status else None,
               stream_of(q))

@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._util import StatusWord, cache_dims, ptr, require, require_cuda, stream_of
+from ._util import StatusWord, cache_dims, check_block_table, ptr, require, require_cuda, stream_of
 
 
 def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
@@ -45,7 +45,7 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
         require(q_out, torch.float16, "q_out")
         if q_out.shape != q.shape:
             raise ValueError("q_out must have q's shape")
-    require(block_table, torch.int32, "block_table")
+    check_block_table(block_table, engine_config)
     if (q_norm is None) != (k_norm is None):
         raise ValueError("pass both q_norm and k_norm, or neither")
     if q_norm is not None:

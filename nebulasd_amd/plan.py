@@ -81,7 +81,7 @@ def decode_plan(words: np.ndarray) -> dict:
     op, oc = int(h[_lib.PLAN_OFF_PIECES]), int(h[_lib.PLAN_OFF_COMBINES])
     table = words[ow:ow + WORKER_WORDS * n_workers].reshape(n_workers, WORKER_WORDS)
     # {kv head, blk_begin, blk_end, slot, row_start, q_len, seq_id, ctx,
-    #  combine, combine first slot, combine slots, worker's groups so far}
+    #  combine, combine first slot, combine slots, worker's blocks before it}
     records = words[op:op + PIECE_WORDS * n_records].reshape(n_records, PIECE_WORDS)
     used = [i for w in range(n_workers) for i in range(int(table[w, 0]), int(table[w, 1]))]
     counts = [int(table[w, 1] - table[w, 0]) for w in range(n_workers)]
@@ -91,7 +91,9 @@ def decode_plan(words: np.ndarray) -> dict:
         "slots": int(h[_lib.PLAN_SLOTS]),
         "rows_max": int(h[_lib.PLAN_ROWS_MAX]),
         "piece_stride": int(h[_lib.PLAN_PIECE_STRIDE]),
-        "ring_stages": int(h[_lib.PLAN_RING_STAGES]),
+        "bt_rows": int(h[_lib.PLAN_BT_ROWS]),
+        "bt_stride": int(h[_lib.PLAN_BT_STRIDE]),
+        "max_blocks": int(h[_lib.PLAN_MAX_BLOCKS]),
         "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
         # per worker: {first record, end record, <first record>, 0...}
         "workers_table": table,
@@ -121,6 +123,13 @@ class AttnPlan:
     @property
     def n_rows(self) -> int:
         return int(self.host[_lib.PLAN_ROWS])
+
+    def fits(self, num_q_heads: int, num_kv_heads: int, block_table) -> bool:
+        """Whether this plan serves calls with these head counts and block table
+        (the table has the row stride the plan was built for and at least its rows)."""
+        return (self.num_q_heads == num_q_heads and self.num_kv_heads == num_kv_heads
+                and int(self.host[_lib.PLAN_BT_STRIDE]) == block_table.shape[1]
+                and int(self.host[_lib.PLAN_BT_ROWS]) <= block_table.shape[0])
 
     def host_ptr(self):
         return self.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
@@ -171,8 +180,8 @@ def plan_for(infer_state, model_config, engine_config, block_table) -> AttnPlan:
     if getter is not None:
         return getter(model_config, engine_config, block_table)
     plan = getattr(infer_state, "nsd_attn_plan", None)
-    if (plan is not None and plan.num_q_heads == model_config.num_q_heads
-            and plan.num_kv_heads == model_config.num_kv_heads):
+    if plan is not None and plan.fits(model_config.num_q_heads, model_config.num_kv_heads,
+                                      block_table):
         return plan
     npf = int(infer_state.num_prefill_seqs)
     sids = getattr(infer_state, "seq_ids_list", None)

@@ -94,25 +94,21 @@ def test_attention_long_contexts_wide_groups(gpu, q_len):
 
 
 def test_attention_every_layer_and_repeatable(gpu):
-    """Every layer checks against the oracle; a repeated call agrees to within
-    fp32 summation-order rounding (waves claim blocks and merge in the order
-    they finish, so the low bits may differ from call to call)."""
+    """Every layer checks against the oracle; a repeated call gives the same
+    bits (every output is summed in a fixed order, whatever the timing)."""
     w = make_workload("target_verify", 4, device=gpu, pool_blocks=2048, num_layers=4,
                       ctxs=[300, 1000, 77, 2500])
     for layer in range(4):
         o, lse, _ = run_attention(w, layer)
         check_against_oracle(w, layer, o, lse, f"layer {layer}")
-    o2, lse2, _ = run_attention(w, 3)
-    assert ((o.float() - o2.float()).abs() <= 1e-3 + 4e-3 * o.float().abs()).all()
-    assert (lse - lse2).abs().max().item() <= 1e-5
+    for _ in range(3):
+        o2, lse2, _ = run_attention(w, 3)
+        assert torch.equal(o, o2) and torch.equal(lse, lse2)
 
 
 def test_attention_reused_plan_split_segments(gpu):
-    """One plan and workspace across calls: long contexts cut into many pieces.
-
-    The per-segment arrival counters in the workspace must be back at zero
-    after every call, or the next call would merge too early.
-    """
+    """One plan and workspace across calls and layers: long contexts cut into
+    many pieces, whose partials every call rewrites before merging them."""
     w = make_workload("target_verify", 7, device=gpu, pool_blocks=4096, num_layers=3,
                       ctxs=[20000, 33, 9000, 1], q_len=5)
     mc = ModelConfig(w.spec.model)
@@ -125,13 +121,7 @@ def test_attention_reused_plan_split_segments(gpu):
         paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o, lse,
                         validate=True)
         torch.cuda.synchronize()
-        plan = st.attn_plan
-        n_comb = int(plan.host[6])
-        assert n_comb > 0, "the long contexts should be split across workgroups"
-        # workspace: partials, then the arrival counters (256-byte aligned parts)
-        part = -(-int(plan.host[7]) * plan.rows_max * 129 * 4 // 256) * 256
-        counters = plan.workspace[part:part + 4 * n_comb].view(torch.int32)
-        assert int(counters.abs().sum()) == 0
+        assert int(st.attn_plan.host[6]) > 0, "the long contexts should be split across workgroups"
         check_against_oracle(w, layer, o, lse, f"reused plan layer {layer}")
 
 
@@ -183,10 +173,52 @@ def test_attention_bad_block_is_flagged(gpu):
 
 def test_attention_no_rows(gpu):
     mc = ModelConfig(QWEN3_8B)
-    ec = EngineConfig()
+    ec = EngineConfig(max_blocks_per_seq=4)
     cos, sin = rope_cache(128, 1e6, 8, gpu)
     st = build_infer_state([], [], [], mc, cos, sin, gpu)
     kc = torch.zeros((4, 1, 8, 16, 128), dtype=torch.float16, device=gpu)
     q = torch.empty((0, 32, 128), dtype=torch.float16, device=gpu)
     paged_attention(q, kc, kc, torch.zeros((1, 4), dtype=torch.int32, device=gpu), mc, ec, st, 0,
                     torch.empty_like(q))
+
+
+def test_attention_graph_replay_bit_identical(gpu):
+    """A HIP graph of attention calls over every layer replays to the eager
+    results bit for bit, replay after replay, with eager work in between."""
+    w = make_workload("target_verify", 9, device=gpu, pool_blocks=4096, num_layers=3,
+                      ctxs=[3000, 40, 1500, 700, 9], q_len=5)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)
+    st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, w.q.device)
+    outs = [torch.empty_like(w.q) for _ in range(3)]
+    lses = [torch.empty(w.q.shape[:2], dtype=torch.float32, device=gpu) for _ in range(3)]
+
+    def calls():
+        for layer in range(3):
+            paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer,
+                            outs[layer], lses[layer])
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [(o.clone(), l.clone()) for o, l in zip(outs, lses)]
+    assert int(st.attn_plan.host[6]) > 0, "expected split segments (the partial merge launch)"
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            calls()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o, l in zip(outs, lses):
+            o.zero_()
+            l.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(3):
+            assert torch.equal(outs[layer], eager[layer][0]), f"replay {rep} layer {layer} o"
+            assert torch.equal(lses[layer], eager[layer][1]), f"replay {rep} layer {layer} lse"
+        calls()  # eager work between replays
+        torch.cuda.synchronize()
+    check_against_oracle(w, 2, outs[2], lses[2], "graph replay layer 2")

@@ -52,7 +52,7 @@ def _state(w, mc, device, prefill=()):
 def test_store_kvcache_full_pool_bit_exact(gpu):
     """Qwen3-8B pool of 24,576 blocks (14.5 G elements: 64-bit offsets)."""
     w = make_workload("target_verify", 0, device=gpu)
-    mc, ec = ModelConfig(w.spec.model), EngineConfig()
+    mc, ec = ModelConfig(w.spec.model), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     st, _, _ = _state(w, mc, gpu)
     layer = 35
     k = torch.randn((w.rows, 8, 128), device=gpu).half()
@@ -69,7 +69,7 @@ def test_store_kvcache_prefill_and_decode(gpu):
     """Mixed forward: two prefill sequences then decode rows (kvcache_mgmt.py:104-122)."""
     w = make_workload("draft_decode", 1, device=gpu, pool_blocks=4096, num_layers=2,
                       ctxs=[40, 600, 17])
-    mc, ec = ModelConfig(QWEN3_0_6B), EngineConfig()
+    mc, ec = ModelConfig(QWEN3_0_6B), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     prefill = [37, 70]
     bt_np = w.block_table.cpu().numpy()
     # prefill sequences use block-table rows 0 and 1 (their own rows of the table)
@@ -142,7 +142,7 @@ def test_rope_table_matches_oracle(gpu):
 def test_fused_prologue_matches_oracle(gpu, name, model):
     """QK-RMSNorm (gamma ~ U[0.5,1.5]) + RoPE (theta 1e6) + KV store for the new rows."""
     w = make_workload(name, 2, device=gpu)
-    mc, ec = ModelConfig(model), EngineConfig()
+    mc, ec = ModelConfig(model), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     st, _, _ = _state(w, mc, gpu)
     cos_c, sin_c = rope_cache(128, mc.rope_theta, 40960, gpu)
     g = torch.Generator(device=gpu).manual_seed(5)
@@ -182,7 +182,7 @@ def test_strided_prologue_equals_contiguous(gpu, name, model):
     written to q_out, the rotated k (in place) and both cache pools are
     bit-identical to the contiguous entry point's on copies; q is untouched."""
     w = make_workload(name, 3, device=gpu)
-    mc, ec = ModelConfig(model), EngineConfig()
+    mc, ec = ModelConfig(model), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     st, _, _ = _state(w, mc, gpu)
     cos_c, sin_c = rope_cache(128, mc.rope_theta, 40960, gpu)
     g = torch.Generator(device=gpu).manual_seed(6)
@@ -216,7 +216,7 @@ def test_fused_equals_unfused(gpu):
     and each path's cache slots hold exactly the k/v that path produced."""
     w = make_workload("target_verify", 3, device=gpu, pool_blocks=2048, num_layers=2,
                       ctxs=[100, 2000, 5])
-    mc, ec = ModelConfig(QWEN3_8B), EngineConfig()
+    mc, ec = ModelConfig(QWEN3_8B), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     st, cos_c, sin_c = _state(w, mc, gpu)
     g = torch.Generator(device=gpu).manual_seed(6)
     q = torch.randn((w.rows, 32, 128), device=gpu, generator=g).half()
@@ -253,7 +253,7 @@ def test_fused_equals_unfused(gpu):
 
 def test_prologue_bad_seq_is_flagged(gpu):
     w = make_workload("target_verify", 7, device=gpu, pool_blocks=256, num_layers=2, ctxs=[10, 20])
-    mc, ec = ModelConfig(QWEN3_8B), EngineConfig()
+    mc, ec = ModelConfig(QWEN3_8B), EngineConfig(max_blocks_per_seq=w.block_table.shape[1])
     st, cos_c, sin_c = _state(w, mc, gpu)
     st.seq_ids[1] = 50  # outside the block table
     k = torch.randn((w.rows, 8, 128), device=gpu).half()

@@ -59,23 +59,17 @@ def test_error_paths_without_gpu(lib):
     assert lib.nsd_rmsnorm_inplace(None, None, 0, 128, 1e-6, None) == 0
     plan = np.zeros(16, np.int32)
     rc = lib.nsd_paged_attention(None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
-                                 plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, None, 0,
-                                 0.1, None, None)
+                                 1, plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None,
+                                 None, 0, 0.1, None, None)
     assert rc == 1 and "null plan" in _lib.last_error()
     rc = lib.nsd_paged_attention(None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
-                                 plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                 1, plan.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
                                  plan.ctypes.data, None, 0, 0.1, None, None)
     assert rc == 1 and "not a plan" in _lib.last_error()
 
 
 # planner constants (nebulasd_amd/csrc/nsd_common.h, nsd_host.cpp)
-MAX_WORKER_PIECES, MIN_PIECE_BLOCKS, PIECE_COST = 32, 4, 24
-
-
-def ring_stages(rows_max):
-    """Blocks per claimed group for groups of up to rows_max query rows
-    (every shape streams with a one-block ring)."""
-    return 1
+MAX_WORKER_PIECES, MAX_WORKER_BLOCKS, MIN_PIECE_BLOCKS, PIECE_COST = 4, 1024, 4, 3
 
 
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
@@ -147,27 +141,30 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
         assert (recs[w * stride + n:(w + 1) * stride] == 0).all()
         if n:
             assert list(row[2:14]) == list(pieces[ws[w]])
-    # each record counts its worker's groups of ring-depth blocks so far
-    stages = ring_stages(p["rows_max"])
-    assert p["ring_stages"] == stages
+    # each record counts the blocks of its worker's earlier pieces (the offset
+    # of its block ids in the worker's id list)
+    blocks = []
     for w in range(p["workers"]):
         run = 0
         for pc in range(ws[w], ws[w + 1]):
-            run += -(-int(pieces[pc][2] - pieces[pc][1]) // stages)
             assert int(pieces[pc][11]) == run
-    # planner limits: pieces per worker
+            run += int(pieces[pc][2] - pieces[pc][1])
+        blocks.append(run)
+    assert p["max_blocks"] == max(blocks)
+    # planner limits: pieces and blocks per worker
     for w in range(p["workers"]):
-        assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES
-    # near-equal cost per active worker: blocks rounded up to whole groups,
-    # plus 24 per piece; only the last active worker, or one stopped by the
-    # piece limit, may fall short
-    cost = [sum(-(-int(pieces[pc][2] - pieces[pc][1]) // stages) * stages + PIECE_COST
-                for pc in range(ws[w], ws[w + 1])) for w in range(p["workers"])]
+        assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES and blocks[w] <= MAX_WORKER_BLOCKS
+    # near-equal cost per active worker: blocks plus 3 per piece; only the
+    # last active worker, or one stopped by the piece or block limit, may
+    # fall short
+    cost = [sum(int(pieces[pc][2] - pieces[pc][1]) + PIECE_COST for pc in range(ws[w], ws[w + 1]))
+            for w in range(p["workers"])]
     active = [w for w in range(p["workers"]) if cost[w] > 0]
     top = max(cost[w] for w in active)
     for w in active[:-1]:
-        assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS + stages) or \
-            ws[w + 1] - ws[w] == MAX_WORKER_PIECES, (w, cost[w], top)
+        assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS) or \
+            ws[w + 1] - ws[w] == MAX_WORKER_PIECES or blocks[w] == MAX_WORKER_BLOCKS, \
+            (w, cost[w], top)
     assert p["workers"] % 8 == 0
 
 
@@ -208,10 +205,9 @@ def test_plan_invariants_random(lib, seed):
     for hq, hkv in ((32, 8), (16, 8), (8, 8)):
         p, ws = _plan(seq_ids, seq_lens, hq, hkv, workers, bt_rows=100)
         check_plan_invariants(p, seq_ids, seq_lens, hkv, hq // hkv)
-        # partials (fp32 O + lse per slot row) then one arrival counter per combine
+        # partials: fp32 O + lse per slot row
         part = -(-p["slots"] * p["rows_max"] * 129 * 4 // 256) * 256
-        cnt = -(-4 * len(p["combines"]) // 256) * 256
-        assert ws == (part + cnt if len(p["combines"]) else 0)
+        assert ws == (part if len(p["combines"]) else 0)
 
 
 def test_plan_splits_long_groups(lib):
@@ -290,13 +286,16 @@ def test_plan_respects_kernel_limits(lib):
     p, _ = _plan(list(range(n)), [1] * n, hq=16, hkv=8, workers=8, bt_rows=n, stride=16)
     check_plan_invariants(p, list(range(n)), [1] * n, 8, 2)
     assert p["workers"] > 8
-    # one long request on one worker: one piece per kv head
+    # one long request asked onto one worker: no worker streams more than
+    # 1024 blocks (its LDS id list), so the 8 x 4000 blocks take 32 workers
     p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
-    assert len(p["pieces"]) == 8 and len(p["combines"]) == 0
+    assert p["max_blocks"] == MAX_WORKER_BLOCKS
+    assert sum(1 for w in range(p["workers"]) if p["worker_start"][w + 1] > p["worker_start"][w]) \
+        == 32
 
 
-def _attention_with_plan(lib, words, hq=32, hkv=8, bt_stride=4096):
+def _attention_with_plan(lib, words, hq=32, hkv=8, bt_rows=2, bt_stride=4096):
     """Call nsd_paged_attention with host buffers standing in for device ones.
 
     Only the host-side plan checks run: every call here must be rejected
@@ -306,16 +305,16 @@ def _attention_with_plan(lib, words, hq=32, hkv=8, bt_stride=4096):
     p = buf.ctypes.data + (-buf.ctypes.data) % 16
     ws = np.zeros(1 << 22, np.uint8)
     wp = ws.ctypes.data + (-ws.ctypes.data) % 16
-    return lib.nsd_paged_attention(p, p, None, p, p, 1000, 2, 0, hq, hkv, 128, 16, p, bt_stride,
-                                   words.ctypes.data_as(i32p), p, wp, ws.size - 16, 128 ** -0.5,
-                                   None, None)
+    return lib.nsd_paged_attention(p, p, None, p, p, 1000, 2, 0, hq, hkv, 128, 16, p, bt_rows,
+                                   bt_stride, words.ctypes.data_as(i32p), p, wp, ws.size - 16,
+                                   128 ** -0.5, None, None)
 
 
 @pytest.mark.skipif(Path("/dev/kfd").exists(),
                     reason="passes host buffers as device pointers: only where no GPU can run it")
 def test_attention_rejects_corrupt_plans(lib):
     """The kernel claims blocks from the records it is given: the launch
-    checks stride, ring depth, group counts, slots and row counts first."""
+    checks stride, block counts, block-table shape, slots and row counts first."""
     from nebulasd_amd import _lib
     from nebulasd_amd.plan import PIECE_WORDS, plan_words
 
@@ -332,10 +331,11 @@ def test_attention_rejects_corrupt_plans(lib):
         return w
 
     cases = [
-        (corrupt(_lib.PLAN_RING_STAGES, 3), "header"),
+        (corrupt(_lib.PLAN_MAX_BLOCKS, 0), "header"),
         (corrupt(_lib.PLAN_PIECE_STRIDE, 0), "header"),
         (corrupt(_lib.PLAN_PIECES, int(h[_lib.PLAN_PIECES]) + 1), "header"),
-        (corrupt(op + 11, words[op + 11] + 1), "piece 0"),                      # group count
+        (corrupt(op + 11, words[op + 11] + 1), "piece 0"),                      # block offset
+        (corrupt(op + 6, 2), "piece 0"),                                        # seq_id past the table
         (corrupt(op + 2, 4096 * 2), "piece 0"),                                 # past the block table row
         (corrupt(op + 5, 64), "piece 0"),                                       # q_len * gqa > rows_max
         (corrupt(op + PIECE_WORDS * split + 3, int(h[_lib.PLAN_SLOTS])), f"piece {split}"),
@@ -361,12 +361,26 @@ def test_noalloc_rejects_plans_larger_than_its_scratch(lib):
     slots, rows_max = int(words[_lib.PLAN_SLOTS]), int(words[_lib.PLAN_ROWS_MAX])
     assert slots * rows_max * 129 * 4 > (16 << 20), "the plan should not fit the scratch"
     rc = lib.nsd_paged_attention_noalloc(
-        None, None, None, None, None, 24576, 36, 0, 32, 8, 128, 16, None, 2100,
+        None, None, None, None, None, 24576, 36, 0, 32, 8, 128, 16, None, 32, 2100,
         words.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, 0.088, None, None)
     assert rc == _lib.NSD_ERR_WORKSPACE and "static scratch" in _lib.last_error()
     # not a plan: rejected as such
     bad = np.zeros(_lib.PLAN_HEADER_WORDS, np.int32)
     rc = lib.nsd_paged_attention_noalloc(
-        None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1,
+        None, None, None, None, None, 1, 1, 0, 32, 8, 128, 16, None, 1, 1,
         bad.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, 0.088, None, None)
     assert rc == 1 and "not a plan" in _lib.last_error()
+
+
+@pytest.mark.skipif(Path("/dev/kfd").exists(),
+                    reason="passes host buffers as device pointers: only where no GPU can run it")
+def test_attention_rejects_plan_for_another_block_table(lib):
+    """A plan checked against one block-table shape is refused for a table
+    with another row stride or fewer rows (its seq_ids could fall outside)."""
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import plan_words
+
+    words, _ = plan_words([0, 1], [300, 900], 32, 8, 128, 16, 2, 4096, 16)
+    for rows, stride in ((1, 4096), (2, 2048)):
+        assert _attention_with_plan(lib, words, bt_rows=rows, bt_stride=stride) == 1
+        assert "block table" in _lib.last_error()

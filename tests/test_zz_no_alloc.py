@@ -32,7 +32,8 @@ def noalloc_call(w, st, mc, layer, o, lse):
               w.q.data_ptr(), o.data_ptr(), lse.data_ptr(), w.k_cache.data_ptr(),
               w.v_cache.data_ptr(), w.k_cache.shape[0], w.k_cache.shape[1], layer,
               mc.num_q_heads, mc.num_kv_heads, 128, 16, w.block_table.data_ptr(),
-              w.block_table.shape[1], plan.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+              w.block_table.shape[0], w.block_table.shape[1],
+              plan.host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
               plan.dev.data_ptr(), float(st.softmax_scale), None, stream_of(w.q))
 
 
