@@ -1,22 +1,30 @@
 """Benchmark of the verify/decode paged-attention layer call on one MI355X.
 
-A step is one layer call of verify attention (Qwen3-8B shape, B=16,
-q_len=5, contexts U[256, 4096], 24,576-block pool, fp16) on inputs already
-resident in HBM.  Steps cycle ``cur_layer`` over all 36 layers so the
-~144 MB per-layer working set cannot stay in the 256 MB Infinity Cache.
-The timed steps are replayed from a HIP graph of one pass over the layers
-(no host launch overhead inside the timed region), timed with HIP events
-on the stream the kernels run on: the mean over all timed calls is the
-headline, and the per-replay median / p10 / p90 and a same-layer "hot"
-figure (every call on layer 0, so its blocks stay cached) are reported as
-diagnostics.  The fused prologue (QK-RMSNorm + RoPE + KV store) is timed
-alone and together with the attention.  Secondary entries measure Draft
-decode (Qwen3-0.6B shape, B=64), ragged long-context verify (q_len=9,
-contexts log-U[1024, 32768]) and the small 4-request decode case, and the
-prefill attention of one 16-prompt chunk (prompts U[128, 1024], both model
-shapes) with its MFMA roofline and the reference's per-prompt SDPA loop
-timed beside it.  The CPU baseline times the numpy oracle on the same inputs
-on this host's cores, median per layer call, for every workload.
+A step is one pass over the model's layers: one verify-attention layer call
+per layer (Qwen3-8B shape: 36 calls; B=16, q_len=5, contexts U[256, 4096],
+24,576-block pool, fp16) on inputs already resident in HBM.  Cycling
+``cur_layer`` over all 36 layers keeps the ~158 MB per-layer working set from
+staying in the 256 MB Infinity Cache.  A HIP graph of one pass is replayed
+``--warmup`` times untimed, then ``--steps`` times timed, with HIP events on
+the stream the kernels run on: ``value`` is µs per layer call (all timed
+calls), ``ms_per_step`` ms per pass, and the per-pass median / p10 / p90 are
+reported beside it, with a same-layer "hot" figure (every call on layer 0,
+whose blocks stay cached) as a diagnostic.  The fused prologue (QK-RMSNorm +
+RoPE + KV store) is timed alone and together with the attention.
+
+Beside the headline: Draft decode (Qwen3-0.6B shape, B=64), ragged
+long-context verify (q_len=9, contexts log-U[1024, 32768]) and the small
+4-request decode case; the attention at the shapes the single-GPU
+speculative loop produces (Qwen3-0.6B draft batch 64 + Qwen3-8B target
+batch 16, depth 4, prompts U[128, 1024]); the prefill attention of one
+16-prompt chunk (both model shapes) with its MFMA roofline and the
+reference's per-prompt SDPA loop; the rest-of-layer kernels, the block-table
+writer and the HostKV copies; and two ceiling probes -- a contiguous
+streaming read and a gather of exactly the K/V tiles each attention workload
+reads, with no arithmetic -- so that the attention's rate can be read
+against what the device delivers for the same bytes.  The CPU baseline runs
+the PyTorch-CPU fp32 restatement of the reference's row-wise attention on
+this host's affinity cores, median per layer call, for every workload.
 
 Prints one JSON line (see ``--help``).
 """
@@ -39,8 +47,9 @@ HBM_PEAK_GBPS = 8000.0
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=1440, help="timed layer calls (multiple of the layer count)")
-    p.add_argument("--warmup", type=int, default=72)
+    p.add_argument("--steps", type=int, default=30,
+                   help="timed passes; a pass is one attention call per layer of the model")
+    p.add_argument("--warmup", type=int, default=3, help="untimed passes before the timed ones")
     p.add_argument("--workload", default="target_verify")
     p.add_argument("--secondary", default="draft_decode,ragged_verify,cpu_plumbing",
                    help="comma-separated workloads measured beside the headline ('' to skip)")
@@ -50,6 +59,9 @@ def parse_args():
     p.add_argument("--hostkv", type=int, default=1, help="1: time the HostKV block-range copies")
     p.add_argument("--layer-rest", type=int, default=1, help="1: time the rest-of-layer kernels")
     p.add_argument("--layer-step", type=int, default=1, help="1: time one whole target-verify layer")
+    p.add_argument("--spec-loop", type=int, default=1,
+                   help="1: time the attention at the speculative loop's shapes (64 requests x 16 tokens)")
+    p.add_argument("--probes", type=int, default=1, help="1: run the HBM ceiling probes")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-baseline-seconds", type=float, default=12.0,
                    help="bound on CPU oracle time (0 disables the CPU baseline)")
@@ -96,7 +108,7 @@ def _spread(per_replay, calls_per_replay: int) -> dict:
 
 
 def measure(name: str, seed: int, steps: int, warmup: int):
-    """Time `steps` layer calls of workload `name`; returns (result dict, workload).
+    """Time `steps` passes over the layers for workload `name`; returns (result dict, workload).
 
     Three graphs of one pass over all layers are timed: the attention alone
     (the headline), the fused prologue alone, and prologue + attention as a
@@ -146,10 +158,10 @@ def measure(name: str, seed: int, steps: int, warmup: int):
             paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, 0, o)
 
     stream = torch.cuda.Stream()
-    reps, wreps = max(1, steps // L), max(1, warmup // L)
+    reps, wreps = max(1, steps), max(0, warmup)
     t0 = time.perf_counter()
-    us, per = _time_graph(attn_pass, stream, reps, wreps)
-    us /= L
+    us_pass, per = _time_graph(attn_pass, stream, reps, wreps)
+    us = us_pass / L
     wall = time.perf_counter() - t0
     us_pro, per_pro = _time_graph(prologue_pass, stream, reps, wreps)
     us_layer, per_layer = _time_graph(layer_pass, stream, reps, wreps)
@@ -161,7 +173,9 @@ def measure(name: str, seed: int, steps: int, warmup: int):
     plan = st.attn_plan
     res = {
         "workload": name,
-        "steps": reps * L,
+        "steps": reps,
+        "layer_calls": reps * L,
+        "us_per_pass": us_pass,
         "us_per_layer_call": us,
         "wall_ms": wall * 1e3,
         "algorithmic_bytes": nbytes,
@@ -222,7 +236,7 @@ def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: 
         return torch.cat(outs)
 
     stream = torch.cuda.Stream()
-    reps, wreps = max(1, steps // calls), max(1, warmup // calls)
+    reps, wreps = max(1, steps), max(0, warmup)
     us, per = _time_graph(kernel_pass, stream, reps, wreps)
     us /= calls
     torch.cuda.synchronize()
@@ -240,7 +254,8 @@ def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: 
     res = {
         "workload": name,
         "kind": "prefill",
-        "steps": reps * calls,
+        "steps": reps,
+        "layer_calls": reps * calls,
         "us_per_layer_call": us,
         "us_per_layer_call_spread": _spread(per, calls),
         "prompts": w.lens,
@@ -259,7 +274,7 @@ def measure_prefill(name: str, seed: int, steps: int, warmup: int, cpu_seconds: 
         from threadpoolctl import threadpool_info, threadpool_limits
 
         q, k, v = (x.cpu().numpy() for x in (w.q, w.k, w.v))
-        cores = min(len(os.sched_getaffinity(0)), 16)
+        cores = _cpu_threads()
         times = []
         with threadpool_limits(limits=cores):
             threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
@@ -827,55 +842,224 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
     return 2 * nbytes / sec / 1e9
 
 
-def cpu_baseline(w, budget_s: float):
-    """Time the numpy oracle (fp32) on the same inputs; bounded to ~budget_s seconds."""
+STREAM_PROBE_BYTES = 4 << 30
+
+
+def stream_read_probe(steps: int) -> dict:
+    """Contiguous read of a 4 GiB buffer (nsd_probe_stream_read): the device's
+    sequential-read rate, mean over `steps` graph replays."""
+    import torch
+
+    from nebulasd_amd import _lib
+
+    buf = torch.empty(STREAM_PROBE_BYTES // 2, dtype=torch.float16, device="cuda")
+    buf.normal_()
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    grid = 16 * torch.cuda.get_device_properties(0).multi_processor_count
+
+    def one():
+        _lib.call("nsd_probe_stream_read", buf.data_ptr(), STREAM_PROBE_BYTES, sink.data_ptr(), grid,
+                  torch.cuda.current_stream().cuda_stream)
+    us, per = _time_graph(one, torch.cuda.Stream(), max(3, steps), 2)
+    del buf
+    torch.cuda.empty_cache()
+    return {"bytes": STREAM_PROBE_BYTES, "us": us, "gbps": STREAM_PROBE_BYTES / us / 1e3,
+            "frac_of_peak": STREAM_PROBE_BYTES / us / 1e3 / HBM_PEAK_GBPS}
+
+
+def attention_tiles(w, layer: int):
+    """Element offsets of the K (= V) tiles one attention call of workload
+    `w` reads at `layer`: every (sequence, kv head, block) its rows reach,
+    ordered by sequence, head, block."""
+    import numpy as np
+
+    n_layers, hkv, bs = w.k_cache.shape[1], w.k_cache.shape[2], w.k_cache.shape[3]
+    tile = bs * w.k_cache.shape[4]
+    bt = w.block_table.cpu().numpy().astype(np.int64)
+    need = {}
+    for sid, n in zip(w.seq_ids, w.seq_lens):
+        need[sid] = max(need.get(sid, 0), (int(n) + bs - 1) // bs)
+    return np.concatenate([((bt[sid, :nb] * n_layers + layer) * hkv + h) * tile
+                           for sid, nb in need.items() for h in range(hkv)])
+
+
+def tile_gather_probe(w, steps: int, warmup: int) -> dict:
+    """The K/V tiles that workload `w`'s attention reads, gathered through an
+    LDS ring with no arithmetic (nsd_probe_tile_gather), split evenly over
+    two workgroups per CU, one launch per layer over all layers: the
+    attention's K/V read floor on this device."""
     import numpy as np
     import torch
-    from threadpoolctl import threadpool_info, threadpool_limits
 
-    import oracle
+    from nebulasd_amd import _lib
 
-    layer = w.spec.num_layers // 2
-    bs = 16
-    bt = w.block_table.cpu().numpy()
-    ids = sorted({int(bt[s, i]) for s, n in zip(w.seq_ids, w.seq_lens) for i in range((n + bs - 1) // bs)})
-    remap = np.zeros(w.k_cache.shape[0], dtype=np.int64)
+    n_layers = w.k_cache.shape[1]
+    per_layer = [attention_tiles(w, layer) for layer in range(n_layers)]
+    n_tiles = len(per_layer[0])
+    workers = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    while -(-n_tiles // workers) > 1536:
+        workers *= 2
+    wstart = np.rint(np.linspace(0, n_tiles, workers + 1)).astype(np.int64)
+    dev = w.k_cache.device
+    tiles = torch.from_numpy(np.concatenate(per_layer)).to(dev)
+    wst = torch.from_numpy(wstart).to(dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    cache_elems = w.k_cache.numel()
+    assert int(tiles.max()) + 2048 <= cache_elems and int(tiles.min()) >= 0
+
+    def one_pass():
+        st = torch.cuda.current_stream().cuda_stream
+        for layer in range(n_layers):
+            _lib.call("nsd_probe_tile_gather", w.k_cache.data_ptr(), w.v_cache.data_ptr(), cache_elems,
+                      tiles.data_ptr() + layer * n_tiles * 8, n_tiles, wst.data_ptr(), workers,
+                      sink.data_ptr(), st)
+    us_pass, per = _time_graph(one_pass, torch.cuda.Stream(), max(1, steps), max(0, warmup))
+    us = us_pass / n_layers
+    kv_bytes = n_tiles * 2 * 2048 * w.k_cache.element_size()
+    return {"tiles_per_layer_call": n_tiles, "kv_bytes": kv_bytes, "workgroups": workers,
+            "us_per_layer_call": us, "us_per_layer_call_spread": _spread(per, n_layers),
+            "gbps": kv_bytes / us / 1e3, "frac_of_peak": kv_bytes / us / 1e3 / HBM_PEAK_GBPS}
+
+
+def measure_spec_loop(seed: int, steps: int, cpu_seconds: float) -> dict:
+    """The attention at the shapes the single-GPU speculative loop produces.
+
+    Runs the loop (random-init Qwen3-0.6B draft + Qwen3-8B target, draft
+    batch 64, target batch 16, depth 4, prompts U[128, 1024]) over 64
+    requests x 16 generated tokens; every 5th forward hands its mid-depth
+    attention call to a timer that replays a HIP graph of that forward's
+    attention over all of the model's layers (`steps` timed passes, the
+    forward's own rows, lengths and caches).  Reports µs per layer call at
+    the observed draft and target shapes, the CPU baseline at one sampled
+    shape of each, and the loop's own counters.
+    """
+    import numpy as np
+    import torch
+
+    from nebulasd_amd.infer_state import build_infer_state
+    from nebulasd_amd.kernels import paged_attention
+    from nebulasd_amd.spec_loop import run
+
+    dev = torch.device("cuda:0")
+    samples = {"draft": [], "target": []}
+    cpu = {}
+    stream = torch.cuda.Stream()
+
+    def make_timer():
+        def timer(model, layer, q, o, lse, seq_ids, seq_lens):
+            mc = model.mc
+            role = "draft" if mc.num_layers == 28 else "target"
+            st = build_infer_state(seq_ids, seq_lens, [], mc, model.cos, model.sin, dev)
+            out = torch.empty_like(q)
+
+            def attn_pass():
+                for li in range(mc.num_layers):
+                    paged_attention(q, model.k_cache, model.v_cache, model.block_table, mc, model.ec,
+                                    st, li, out)
+            us_pass, _ = _time_graph(attn_pass, stream, max(1, steps // 4), 1)
+            us = us_pass / mc.num_layers
+            per_seq = {}
+            for sid, n in zip(seq_ids, seq_lens):
+                per_seq[sid] = max(per_seq.get(sid, 0), n)
+            hkv, hq = mc.num_kv_heads, mc.num_q_heads
+            kv_tokens = sum(per_seq.values())
+            nbytes = (kv_tokens * hkv * 128 * 2 * 2 + len(seq_ids) * hq * 128 * 2 * 2
+                      + sum((n + 15) // 16 for n in per_seq.values()) * 4)
+            _, counts = np.unique(np.asarray(seq_ids), return_counts=True)
+            samples[role].append({"rows": len(seq_ids), "max_q_len": int(counts.max()),
+                                  "kv_tokens": kv_tokens, "us_per_layer_call": us,
+                                  "gbps": nbytes / us / 1e3})
+            if cpu_seconds > 0 and role not in cpu and len(seq_ids) == (64 if role == "draft" else 80):
+                cpu[role] = cpu_attention_baseline(q, model.k_cache, model.v_cache, model.block_table,
+                                                   seq_ids, seq_lens, layer, cpu_seconds,
+                                                   f"the loop's {role} forward ({len(seq_ids)} rows)")
+        return timer
+
+    t0 = time.perf_counter()
+    res = run(n_requests=64, prompt_lo=128, prompt_hi=1024, new_tokens=16, draft_batch=64,
+              target_batch=16, depth=4, seed=seed, check_every=5, make_check=make_timer, device=dev)
+    wall = time.perf_counter() - t0
+    out = {"workload": "spec_loop_shapes", "loop": {k: v for k, v in res.items()},
+           "bench_wall_s": wall}
+    for role, xs in samples.items():
+        if not xs:
+            continue
+        us = np.array([x["us_per_layer_call"] for x in xs])
+        out[role] = {"samples": len(xs), "us_per_layer_call_median": float(np.median(us)),
+                     "us_per_layer_call_min": float(us.min()), "us_per_layer_call_max": float(us.max()),
+                     "gbps_median": float(np.median([x["gbps"] for x in xs])),
+                     "rows": sorted({x["rows"] for x in xs}),
+                     "kv_tokens_median": float(np.median([x["kv_tokens"] for x in xs])),
+                     "cpu_baseline": cpu.get(role)}
+    torch.cuda.empty_cache()
+    return out
+
+
+def _cpu_threads() -> int:
+    """The host cores this process may run on (its CPU affinity)."""
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_attention_baseline(q, k_cache, v_cache, block_table, seq_ids, seq_lens, layer: int,
+                           budget_s: float, what: str) -> dict:
+    """Time the PyTorch-CPU fp32 restatement of the reference's row-wise
+    attention (oracle/attention_torch.py) on the referenced blocks of one
+    layer, on every affinity core; median of calls within ~budget_s seconds."""
+    import numpy as np
+    import torch
+
+    from oracle.attention_torch import paged_attention_rowwise
+
+    bs = k_cache.shape[3]
+    bt = block_table.cpu().numpy()
+    ids = sorted({int(bt[s, i]) for s, n in zip(seq_ids, seq_lens) for i in range((n + bs - 1) // bs)})
+    remap = np.zeros(k_cache.shape[0], dtype=np.int64)
     remap[ids] = np.arange(len(ids))
-    idx = torch.tensor(ids, device=w.k_cache.device)
-    kc = w.k_cache[idx, layer].unsqueeze(1).cpu().numpy()
-    vc = w.v_cache[idx, layer].unsqueeze(1).cpu().numpy()
-    bt_s = remap[bt]
-    q = w.q.cpu().numpy()
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    idx = torch.tensor(ids, device=k_cache.device)
+    kc = k_cache[idx, layer].unsqueeze(1).cpu()
+    vc = v_cache[idx, layer].unsqueeze(1).cpu()
+    bt_s = torch.from_numpy(remap[bt])
+    qc = q.cpu()
+    threads_before = torch.get_num_threads()
+    cores = _cpu_threads()
+    torch.set_num_threads(cores)
     times = []
-    with threadpool_limits(limits=cores):
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    try:
         t_end = time.perf_counter() + budget_s
         while True:
             t0 = time.perf_counter()
-            oracle.paged_attention(q, kc, vc, bt_s, w.seq_ids, w.seq_lens, 0, dtype=np.float32)
+            paged_attention_rowwise(qc, kc, vc, bt_s, seq_ids, seq_lens, 0)
             times.append(time.perf_counter() - t0)
             if time.perf_counter() > t_end or len(times) >= 20:
                 break
-    us = float(np.median(times)) * 1e6
+        used = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(threads_before)
     return {
-        "value": us,
+        "value": float(np.median(times)) * 1e6,
         "unit": "us/layer-call",
-        "cores": int(min(threads, cores)),
+        "cores": int(used),
+        "affinity_cores": cores,
         "kind": "port",
-        "sample": f"{len(times)} layer calls of {w.spec.name} (one layer, same seeded inputs), "
-                  f"numpy fp32 oracle, median",
+        "sample": f"{len(times)} layer calls of {what} (one layer, the same inputs as the GPU run), "
+                  "PyTorch-CPU fp32 row-wise attention, median",
         "cpu_model": _cpu_model(),
     }
 
 
+def cpu_baseline(w, budget_s: float):
+    """CPU baseline of workload `w` at its middle layer."""
+    return cpu_attention_baseline(w.q, w.k_cache, w.v_cache, w.block_table, w.seq_ids, w.seq_lens,
+                                  w.spec.num_layers // 2, budget_s, w.spec.name)
+
+
 def _cpu_time(fn, budget_s: float, max_reps: int = 20, what: str = "") -> dict:
-    """Median wall time of fn() on the host cores (at most 16 threads), at
-    least one call and about `budget_s` seconds."""
+    """Median wall time of fn() on the affinity cores, at least one call and
+    about `budget_s` seconds."""
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = _cpu_threads()
     times = []
     with threadpool_limits(limits=cores):
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
@@ -919,9 +1103,18 @@ def main():
 
         build()
     copy_gbps = copy_probe()
+    probes = {"copy_gbps": copy_gbps}
+    if args.probes:
+        probes["stream_read"] = stream_read_probe(args.steps)
+        print(f"# probes: contiguous read {probes['stream_read']['gbps']:.0f} GB/s, copy {copy_gbps:.0f} GB/s",
+              file=sys.stderr, flush=True)
     res, w = measure(args.workload, args.seed, args.steps, args.warmup)
+    if args.probes:
+        res["kv_gather_floor"] = tile_gather_probe(w, args.steps, args.warmup)
+        res["frac_of_gather_floor"] = res["kv_gather_floor"]["us_per_layer_call"] / res["us_per_layer_call"]
     print(f"# {args.workload}: {res['us_per_layer_call']:.2f} us/layer-call, "
-          f"{res['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+          f"{res['hbm_gbps']:.0f} GB/s" + (f" (K/V gather floor {res['kv_gather_floor']['us_per_layer_call']:.2f} us)"
+                                          if args.probes else ""), file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_baseline_seconds > 0:
         cpu = cpu_baseline(w, args.cpu_baseline_seconds)
@@ -971,6 +1164,9 @@ def main():
         secondary[r2["workload"]] = r2
     for name in filter(None, args.secondary.split(",")):
         r2, w2 = measure(name, args.seed, args.steps, args.warmup)
+        if args.probes:
+            r2["kv_gather_floor"] = tile_gather_probe(w2, args.steps, args.warmup)
+            r2["frac_of_gather_floor"] = r2["kv_gather_floor"]["us_per_layer_call"] / r2["us_per_layer_call"]
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
               f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
         if args.cpu_baseline_seconds > 0:
@@ -978,6 +1174,12 @@ def main():
         secondary[name] = r2
         del w2
         torch.cuda.empty_cache()
+    if args.spec_loop:
+        r2 = measure_spec_loop(args.seed, args.steps, args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
+        print("# speculative loop shapes: " + "; ".join(
+            f"{role} {r2[role]['us_per_layer_call_median']:.1f} us/layer-call over {r2[role]['samples']} forwards"
+            for role in ("draft", "target") if role in r2), file=sys.stderr, flush=True)
+        secondary[r2["workload"]] = r2
     line = {
         "metric": "verify/decode attn µs per layer + HBM GB/s (% peak), Qwen3-8B B=16 q_len=5",
         "value": res["us_per_layer_call"],
@@ -985,7 +1187,7 @@ def main():
         "n_gpus": 1,
         "steps": res["steps"],
         "warmup": args.warmup,
-        "ms_per_step": res["us_per_layer_call"] / 1e3,
+        "ms_per_step": res["us_per_pass"] / 1e3,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -994,7 +1196,8 @@ def main():
         "config": {
             "workload": f"{args.workload}: Qwen3-8B attention shape (32q/8kv heads, d=128), B={spec.batch}, "
                         f"q_len={spec.q_len}, contexts {spec.ctx[0]} [{spec.ctx[1]},{spec.ctx[2]}], "
-                        f"block 16, pool {spec.pool_blocks} blocks, layers cycled 0..{spec.num_layers - 1}",
+                        f"block 16, pool {spec.pool_blocks} blocks, layers cycled 0..{spec.num_layers - 1}; "
+                        f"a step is one pass of {spec.num_layers} layer calls",
             "batch": spec.batch,
             "q_len": spec.q_len,
             "seed": args.seed,
@@ -1009,8 +1212,10 @@ def main():
             "unit": "GB/s",
             "frac": res["hbm_frac"],
             "traffic": traffic_from_profiles(args.workload),
+            "kernels": "paged_attn_kernel (+ combine_kernel for split segments), one layer call",
         },
         "copy_probe_gbps": copy_gbps,
+        "probes": probes,
         "cpu_baseline": cpu,
         "detail": res,
         "secondary": secondary,

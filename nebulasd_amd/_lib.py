@@ -90,6 +90,9 @@ SIGNATURES = {
     "nsd_silu_and_mul_inplace": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "nsd_lm_head_argmax": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "nsd_argmax_rows": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "nsd_probe_stream_read": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
+    "nsd_probe_tile_gather": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p, c_void_p]),
     "nsd_prefill_attention": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                 c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),

@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "_lib"
 LIB_PATH = LIB_DIR / "libnsd_attn.so"
-SOURCES = ["nsd_host.cpp", "nsd_prologue.hip", "nsd_attention.hip", "nsd_prefill.hip", "nsd_blocks.hip", "nsd_hostkv.hip", "nsd_layer.hip"]
+SOURCES = ["nsd_host.cpp", "nsd_prologue.hip", "nsd_attention.hip", "nsd_prefill.hip", "nsd_blocks.hip", "nsd_hostkv.hip", "nsd_layer.hip", "nsd_probe.hip"]
 ARCH = "gfx950"
 
 

@@ -165,14 +165,26 @@ class RandomQwen3:
         return self._forward(st, tokens, attention)
 
 
+def _sync(dev: torch.device) -> None:
+    if dev.type == "cuda":
+        torch.cuda.synchronize(dev)
+
+
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
         target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
-        draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, log=None) -> dict:
+        draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, share_weights=False, return_outputs=False,
+        log=None) -> dict:
     """The speculative loop over `n_requests` synthetic requests; returns a summary.
 
     With ``check_every`` > 0, every check_every-th forward calls
     ``make_check()(model, layer, q, o, lse, seq_ids, seq_lens)`` for its
-    mid-depth attention layer call.
+    mid-depth attention layer call.  ``share_weights`` builds the draft with
+    the target's configuration and seed, so that it holds the same weights
+    and its greedy proposals are accepted except where the two forwards'
+    rounding splits a near-tie: this exercises multi-token acceptance and
+    the draft's two-row reconcile step, which independent random models
+    (acceptance 0) never reach.  ``return_outputs`` adds every request's
+    generated tokens to the summary (key ``outputs``).
     """
     dev = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -182,7 +194,10 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     # room for the prompt, the output and one proposal beyond it
     blocks = [math.ceil((p + new_tokens + depth + 2) / 16) for p in plens]
     target = RandomQwen3(target_cfg, blocks, dev, seed + 1)
-    draft = RandomQwen3(draft_cfg, blocks, dev, seed + 2)
+    if share_weights:
+        draft = RandomQwen3(target_cfg, blocks, dev, seed + 1)
+    else:
+        draft = RandomQwen3(draft_cfg, blocks, dev, seed + 2)
     n_checks = 0
     t0 = time.perf_counter()
 
@@ -196,13 +211,14 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
             out[r].append(t)
         if log and (s // chunk) % 8 == 7:
             log(f"prefill: {ids[-1] + 1} of {n_requests} requests")
-    torch.cuda.synchronize()
+    _sync(dev)
     t_prefill = time.perf_counter() - t0
     # tokens of the output each cache holds: the target all but the anchor;
     # the draft the same, or one fewer after a fully accepted proposal
     draft_missing = [None] * n_requests  # accepted proposal token the draft has not run
     stats = {"target_forwards": 0, "draft_forwards": 0, "rounds": 0, "proposed": 0,
-             "accepted": 0}
+             "accepted": 0, "reconcile_groups": 0, "full_accepts": 0, "partial_accepts": 0,
+             "multi_token_appends": 0}
     step = 0
     while True:
         live = [r for r in range(n_requests) if len(out[r]) < new_tokens]
@@ -218,6 +234,7 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                 for r in dgroup:
                     base = plens[r] + len(out[r]) - 1 + j  # tokens before this step's input
                     if j == 0 and draft_missing[r] is not None:
+                        stats["reconcile_groups"] += 1
                         sids += [r, r]
                         slens += [base, base + 1]
                         toks += [draft_missing[r], out[r][-1]]
@@ -257,20 +274,26 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                     acc, n_acc = compute_greedy_acceptance(props[r], p, new_tokens - len(out[r]))
                     stats["proposed"] += depth
                     stats["accepted"] += n_acc
+                    stats["full_accepts"] += n_acc == depth
+                    # a proposal token rejected after at least one accepted (not a
+                    # proposal cut short by the output limit: len(acc) == n_acc then)
+                    stats["partial_accepts"] += 0 < n_acc < depth and len(acc) == n_acc + 1
+                    stats["multi_token_appends"] += len(acc) > 1
                     if n_acc == depth and len(acc) == depth + 1:
                         draft_missing[r] = props[r][-1]
                     out[r] += acc
         if log:
             log(f"round {stats['rounds']}: {sum(min(len(o), new_tokens) for o in out)} tokens")
-    torch.cuda.synchronize()
+    _sync(dev)
     wall = time.perf_counter() - t0
     generated = sum(len(o) for o in out)
+    extra = {"outputs": out} if return_outputs else {}
     return {
         "requests": n_requests, "new_tokens": new_tokens, "generated_tokens": generated,
         "prompt_tokens": int(sum(plens)), "wall_s": wall, "prefill_s": t_prefill,
         "decode_tokens_per_s": (generated - n_requests) / max(wall - t_prefill, 1e-9),
         "acceptance_rate": stats["accepted"] / max(stats["proposed"], 1), **stats,
-        "attention_checks": n_checks,
+        "attention_checks": n_checks, **extra,
     }
 
 
@@ -284,9 +307,11 @@ def main():
     p.add_argument("--target-batch", type=int, default=16)
     p.add_argument("--depth", type=int, default=4)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--share-weights", action="store_true",
+                   help="draft = the target's model and weights (proposals accepted)")
     a = p.parse_args()
     res = run(a.requests, a.prompt_lo, a.prompt_hi, a.new_tokens, a.draft_batch, a.target_batch,
-              a.depth, a.seed, log=lambda m: print(m, flush=True))
+              a.depth, a.seed, share_weights=a.share_weights, log=lambda m: print(m, flush=True))
     print(json.dumps(res), flush=True)
 
 

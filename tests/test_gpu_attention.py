@@ -46,8 +46,8 @@ def check_against_oracle(w, layer, o, lse, what):
     print(f"{what}: max|do|={e_o:.2e} max|dlse|={e_l:.2e}", flush=True)
 
 
-CASES = [("cpu_plumbing", 0), ("cpu_plumbing", 1), ("cpu_plumbing", 2), ("draft_decode", 0),
-         ("target_verify", 0), ("target_verify", 1), ("ragged_verify", 0)]
+CASES = [("cpu_plumbing", 0), ("cpu_plumbing", 1), ("cpu_plumbing", 2)] + \
+    [(n, s) for n in ("draft_decode", "target_verify", "ragged_verify") for s in range(5)]
 
 
 @pytest.mark.parametrize("name,seed", CASES, ids=[f"{n}-s{s}" for n, s in CASES])
@@ -222,3 +222,57 @@ def test_attention_graph_replay_bit_identical(gpu):
         calls()  # eager work between replays
         torch.cuda.synchronize()
     check_against_oracle(w, 2, outs[2], lses[2], "graph replay layer 2")
+
+
+def test_attention_mixed_prefill_forward(gpu):
+    """A forward with prefill sequences first: the wrapper is given the decode
+    rows' slices ``q[num_prefill_tokens:]`` / ``o[num_prefill_tokens:]`` and
+    reads ``seq_ids[num_prefill_seqs:]`` (transformer_layer.py:171-179,
+    paged_attn.py:197); the prefill part of ``o`` is left alone."""
+    w = make_workload("target_verify", 10, device=gpu, pool_blocks=2048, num_layers=2,
+                      ctxs=[900, 12, 2000, 333, 50, 1], q_len=5)
+    mc = ModelConfig(w.spec.model)
+    ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+    prefill_lens = [37, 5, 120]
+    prefill_ids = [3, 0, 5]  # rows of the block table, as the engine assigns them
+    npt = sum(prefill_lens)
+    cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)
+    st = build_infer_state(prefill_ids + list(w.seq_ids), w.seq_lens, prefill_lens, mc, cos, sin,
+                           w.q.device)
+    assert st.num_prefill_seqs == 3 and st.num_prefill_tokens == npt
+    hq, d = w.q.shape[1:]
+    q = torch.randn((npt + w.rows, hq, d), device=gpu).half()
+    q[npt:] = w.q
+    o = torch.full((npt + w.rows, hq * d), 7.0, dtype=torch.float16, device=gpu)
+    lse = torch.empty((w.rows, hq), dtype=torch.float32, device=gpu)
+    paged_attention(q[npt:], w.k_cache, w.v_cache, w.block_table, mc, ec, st, 1, o[npt:], lse,
+                    validate=True)
+    torch.cuda.synchronize()
+    assert bool((o[:npt] == 7.0).all()), "the prefill rows of o were written"
+    check_against_oracle(w, 1, o[npt:].view(w.rows, hq, d), lse, "mixed forward")
+
+
+def test_attention_interleaved_rows(gpu):
+    """Rows of one sequence that are not adjacent (a, b, a, b ...) are valid
+    reference input; each row attends to its own seq_len prefix."""
+    w = make_workload("target_verify", 11, device=gpu, pool_blocks=2048, num_layers=2,
+                      ctxs=[700, 1500, 64], q_len=1)
+    ctx = w.ctxs
+    seq_ids = [0, 1, 0, 1, 2, 0, 2, 1]
+    nth = {}
+    seq_lens = []
+    for s in seq_ids:
+        nth[s] = nth.get(s, 0) + 1
+        seq_lens.append(ctx[s] - 3 + nth[s])  # rising by one per row of the sequence
+    hq, d = w.q.shape[1:]
+    w.q = torch.randn((len(seq_ids), hq, d), device=gpu).half()
+    w.seq_ids, w.seq_lens = seq_ids, seq_lens
+    o, lse, st = run_attention(w, 1)
+    check_against_oracle(w, 1, o, lse, "interleaved rows")
+    # the same rows, grouped per sequence, give the same per-row results
+    order = sorted(range(len(seq_ids)), key=lambda i: (seq_ids[i], seq_lens[i]))
+    q_interleaved = w.q
+    w.q = q_interleaved[order].contiguous()
+    w.seq_ids, w.seq_lens = [seq_ids[i] for i in order], [seq_lens[i] for i in order]
+    o2, lse2, _ = run_attention(w, 1)
+    check_against_oracle(w, 1, o2, lse2, "same rows grouped")

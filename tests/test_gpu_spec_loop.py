@@ -1,9 +1,12 @@
 """The speculative loop on random-init Qwen3-0.6B (draft) + Qwen3-8B (target).
 
-A reduced run of the single-GPU speculative configuration: full model
-shapes and depth 4, few short requests.  Attention layer calls sampled from
-both models are checked against the oracle; the loop must finish every
-request with exactly the requested number of tokens.
+Runs at the single-GPU speculative configuration's shapes -- draft batch 64,
+target batch 16, depth 4, prompts U[128, 1024] -- with fewer requests and
+output tokens than the full 512 x 128 run, plus a reduced run and a run in
+which the draft holds the target's weights, so that proposals are accepted
+and the multi-token append and the draft's two-row reconcile step execute.
+Attention layer calls sampled from both models are checked against the
+oracle; every request must finish with exactly the requested tokens.
 """
 
 from __future__ import annotations
@@ -14,6 +17,10 @@ from nebulasd_amd.spec_loop import run
 from spec_checks import make_checker
 
 pytestmark = pytest.mark.gpu
+
+
+def progress(msg):
+    print(msg, flush=True)
 
 
 def test_speculative_loop_small(gpu):
@@ -28,3 +35,37 @@ def test_speculative_loop_small(gpu):
     # both models' calls were checked, verify rows (q_len 5) included
     assert {r["layers"] for r in results} == {28, 36}
     assert max(r["max_q_len"] for r in results if r["layers"] == 36) == 5
+
+
+def test_speculative_loop_config_shape(gpu):
+    """Draft batch 64 / target batch 16 / depth 4 over 64 prompts of U[128, 1024] tokens."""
+    results = []
+    res = run(n_requests=64, prompt_lo=128, prompt_hi=1024, new_tokens=16, draft_batch=64,
+              target_batch=16, depth=4, seed=5, check_every=5, make_check=make_checker(results),
+              device=gpu, log=progress)
+    print({k: v for k, v in res.items()}, flush=True)
+    assert res["generated_tokens"] == 64 * 16
+    assert results and all(r["ok"] for r in results), [r for r in results if not r["ok"]]
+    assert {r["layers"] for r in results} == {28, 36}
+    draft_rows = {r["rows"] for r in results if r["layers"] == 28}
+    target_rows = {r["rows"] for r in results if r["layers"] == 36}
+    assert max(draft_rows) == 64 and max(target_rows) == 16 * 5
+    assert max(r["max_seq_len"] for r in results) > 900
+
+
+def test_speculative_loop_shared_weights_accepts(gpu):
+    """The draft holds the target's weights: proposals are accepted, the
+    draft reconciles after fully accepted proposals, and the sampled calls
+    (two-row draft groups among them) still match the oracle."""
+    results = []
+    res = run(n_requests=64, prompt_lo=128, prompt_hi=1024, new_tokens=16, draft_batch=64,
+              target_batch=16, depth=4, seed=6, check_every=2, make_check=make_checker(results),
+              device=gpu, share_weights=True, log=progress)
+    print({k: v for k, v in res.items()}, flush=True)
+    assert res["generated_tokens"] == 64 * 16
+    assert res["acceptance_rate"] > 0.5
+    assert res["full_accepts"] > 0 and res["reconcile_groups"] > 0
+    assert res["multi_token_appends"] > 0
+    assert results and all(r["ok"] for r in results), [r for r in results if not r["ok"]]
+    # a checked draft forward held two-row reconcile groups
+    assert any(r["max_q_len"] == 2 and r["rows"] < 5 * 64 for r in results)

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "nsd_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "speculative_cases.json").read_text())
 
 
@@ -28,7 +28,7 @@ def lib():
 
 
 def header_functions() -> list[str]:
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(nsd_\w+)\(", text, re.M)))
 
 
@@ -38,7 +38,7 @@ def test_library_exports_every_header_symbol(lib):
     names = header_functions()
     assert len(names) >= 11
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in nsd_attn.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert lib.nsd_version() >= 100
 
