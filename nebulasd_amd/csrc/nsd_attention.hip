@@ -9,12 +9,11 @@
 //   S^T[token][row] = K[token][:] . Q[row][:]            (A = K, B = Q^T)
 //   O^T[dim][row]  += V^T[dim][token] . P^T[token][row]  (A = V^T, B = P^T)
 //
-// S^T uses v_mfma_f32_16x16x32_f16 (k = head dim), O^T uses
-// v_mfma_f32_16x16x16_f16 (k = the 16 tokens of one cache block).  Both leave
-// a lane holding one query row (lane & 15) of a 16-row tile, so a row's
-// online-softmax state lives in one lane column, and the S^T result of a
-// block is already the P^T operand of the PV product (lane group g holds
-// tokens 4g..4g+3).
+// Both products use v_mfma_f32_16x16x32_f16: S^T with k = 32 of the 128 head
+// dims per instruction, O^T with k = the 32 tokens of a two-block step.  Both
+// leave a lane holding one query row (lane & 15) of a 16-row tile, so a row's
+// online-softmax state lives in one lane column, and the S^T result of a step
+// is already the P^T operand of the PV product (see the token order below).
 //
 // Work split.  The host planner cuts the stream of (segment, 16-token block)
 // work into contiguous ranges of near-equal cost, one per workgroup
