@@ -86,13 +86,17 @@ def reference_seq_block_size(num_kv_heads: int, decoding_seq_lens_list) -> int:
 
 def build_infer_state(seq_ids_list, decoding_seq_lens_list, prefill_lens_list, model_config,
                       cos_cache: torch.Tensor, sin_cache: torch.Tensor, device,
-                      max_group_rows: int = 0) -> LlamaInferState:
+                      max_group_rows: int = 0, ignore_kvcache: bool = False) -> LlamaInferState:
     """Metadata of one forward (swiftLLM/swiftllm/worker/model.py:325-430).
 
     ``seq_ids_list`` covers prefill sequences first, then decode rows;
     ``prefill_lens_list`` gives the prompt length of each prefill sequence.
+    ``ignore_kvcache`` marks a prefill-only forward that must not write the
+    cache (transformer_layer.py:133); decode rows cannot use it (:171).
     """
     num_prefill = len(prefill_lens_list)
+    if ignore_kvcache and decoding_seq_lens_list:
+        raise ValueError("ignore_kvcache needs a forward without decode rows (they attend the cache)")
     if len(seq_ids_list) != num_prefill + len(decoding_seq_lens_list):
         raise ValueError("seq_ids_list must list prefill sequences then decode rows")
     dev = torch.device(device)
@@ -126,13 +130,38 @@ def build_infer_state(seq_ids_list, decoding_seq_lens_list, prefill_lens_list, m
         seq_ids_list=list(seq_ids_list[num_prefill:]),
         decoding_seq_lens_list=list(decoding_seq_lens_list),
         max_group_rows=max_group_rows,
+        ignore_kvcache=ignore_kvcache,
     )
 
 
-def rope_cache(head_dim: int, theta: float, max_positions: int, device, scaling: float = 1.0):
-    """fp16 cos/sin caches [max_positions, head_dim/2] (model.py:242-252, scalar scaling)."""
+def rope_cache(head_dim: int, theta: float, max_positions: int, device, scaling=1.0):
+    """fp16 cos/sin caches [max_positions, head_dim/2] (model.py:209-252).
+
+    ``scaling`` is the config's ``rope_scaling``: a number divides every
+    position (model.py:242-246); a dict (Llama 3.2 style, model.py:209-240)
+    splits the frequencies at ``int(d/2 * lf / (lf + hf))`` and divides the
+    positions by ``low_freq_factor`` (lf) below the split and by
+    ``high_freq_factor`` (hf) above it.  Positions are the table rows, so
+    ``max_positions`` only sets the length.
+    """
     dev = torch.device(device)
-    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=dev, dtype=torch.float32) / head_dim))
-    t = torch.arange(max_positions, device=dev, dtype=torch.float32) / scaling
-    freqs = torch.outer(t, inv_freq)
+    f32 = dict(device=dev, dtype=torch.float32)
+    t = torch.arange(max_positions, **f32)
+    if isinstance(scaling, dict):
+        lf = float(scaling.get("low_freq_factor", 1.0))
+        hf = float(scaling.get("high_freq_factor", 1.0))
+        split = int((head_dim // 2) * lf / (lf + hf))
+        inv_low = 1.0 / (theta ** (torch.arange(0, split * 2, 2, **f32) / head_dim))
+        inv_high = 1.0 / (theta ** (torch.arange(split * 2, head_dim, 2, **f32) / head_dim))
+        freqs = torch.cat([torch.outer(t / lf, inv_low), torch.outer(t / hf, inv_high)], dim=-1)
+    else:
+        inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, **f32) / head_dim))
+        freqs = torch.outer(t / float(scaling), inv_freq)
     return torch.cos(freqs).to(torch.float16), torch.sin(freqs).to(torch.float16)
+
+
+def model_rope_cache(model_config, max_positions: int, device):
+    """The cos/sin caches of ``model_config`` (its rope_theta, head_dim and
+    rope_scaling, number or dict), ``max_positions`` rows."""
+    return rope_cache(model_config.head_dim, model_config.rope_theta, max_positions, device,
+                      getattr(model_config, "rope_scaling", 1.0) or 1.0)

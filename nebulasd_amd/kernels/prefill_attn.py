@@ -17,21 +17,17 @@ from .. import _lib
 from ._util import StatusWord, ptr, require, require_cuda, stream_of
 
 
-_ORDER_CACHE: dict = {}
-
-
 def _longest_first(cu_seqlens: torch.Tensor) -> torch.Tensor:
     """Prompt indices, longest first (device int32, computed on the device with
-    no host synchronisation; cached per cu_seqlens tensor and version, so the
-    layers of one forward share it)."""
-    key = (cu_seqlens.data_ptr(), cu_seqlens._version, cu_seqlens.numel(), cu_seqlens.device)
-    order = _ORDER_CACHE.get(key)
-    if order is None:
-        lens = cu_seqlens[1:] - cu_seqlens[:-1]
-        order = torch.argsort(lens, descending=True, stable=True).to(torch.int32)
-        if len(_ORDER_CACHE) >= 16:
-            _ORDER_CACHE.clear()
-        _ORDER_CACHE[key] = order
+    no host synchronisation).  Kept on the ``cu_seqlens`` tensor object itself
+    together with its version counter, so the layers of one forward share it
+    and a new or modified tensor gets its own."""
+    cached = getattr(cu_seqlens, "_nsd_longest_first", None)
+    if cached is not None and cached[0] == cu_seqlens._version:
+        return cached[1]
+    lens = cu_seqlens[1:] - cu_seqlens[:-1]
+    order = torch.argsort(lens, descending=True, stable=True).to(torch.int32)
+    cu_seqlens._nsd_longest_first = (cu_seqlens._version, order)
     return order
 
 

@@ -60,6 +60,10 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
         raise ValueError("cos/sin caches must be [max_positions, head_dim/2]")
     if rows == 0:
         return
+    if getattr(infer_state, "ignore_kvcache", False):
+        # the reference stores nothing then, and asserts there are no decode rows
+        # (transformer_layer.py:133, :171); decode rows must store their K/V
+        raise ValueError("infer_state.ignore_kvcache is set but the forward has decode rows")
     npf = infer_state.num_prefill_seqs
     status = StatusWord(q.device) if validate else None
     tail = (ptr(q_norm), ptr(k_norm), float(model_config.rms_norm_eps), cos_cache.data_ptr(), sin_cache.data_ptr(),

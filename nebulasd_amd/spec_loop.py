@@ -48,10 +48,11 @@ import torch
 import torch.nn.functional as F
 
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
-from .infer_state import build_infer_state, rope_cache
+from .infer_state import build_infer_state, model_rope_cache
 from .kernels import (flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention, post_layer_forward,
                       qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace, silu_and_mul_inplace,
                       store_kvcache)
+from .phases import forward_phase_range
 from .speculative import compute_greedy_acceptance
 
 
@@ -94,7 +95,7 @@ class RandomQwen3:
         shape = (n_blocks, mc.num_layers, hkv, 16, d)
         self.k_cache = torch.zeros(shape, dtype=torch.float16, device=dev)
         self.v_cache = torch.zeros(shape, dtype=torch.float16, device=dev)
-        self.cos, self.sin = rope_cache(d, mc.rope_theta, width * 16 + 1, dev)
+        self.cos, self.sin = model_rope_cache(mc, width * 16 + 1, dev)
         self.check = None  # (layer, callback) of a sampled attention check
 
     def _forward(self, st, token_ids: list, attention) -> list:
@@ -109,24 +110,31 @@ class RandomQwen3:
         res = torch.zeros_like(x)
         for li, lw in enumerate(self.layers):
             fused_add_rmsnorm_inplace(x, res, lw["n_in"], eps)
-            qkv = F.linear(x, lw["wqkv"])  # one GEMM for the reference's three (transformer_layer.py:107-109)
+            with forward_phase_range(f"layer_{li}_qkv"):
+                qkv = F.linear(x, lw["wqkv"])  # one GEMM for the reference's three (transformer_layer.py:107-109)
             q = qkv[:, :hq * d].view(-1, hq, d)
             k = qkv[:, hq * d:(hq + hkv) * d].view(-1, hkv, d)
             v = qkv[:, (hq + hkv) * d:].view(-1, hkv, d)
             o = attention(li, lw, q, k, v)
-            o = F.linear(o.view(x.shape[0], -1), lw["wo"])
+            with forward_phase_range(f"layer_{li}_o_proj"):
+                o = F.linear(o.view(x.shape[0], -1), lw["wo"])
             fused_add_rmsnorm_inplace(o, res, lw["n_post"], eps)
-            up_gate = F.linear(o, lw["wug"])
-            silu_and_mul_inplace(up_gate)
-            x = F.linear(up_gate[:, :inter], lw["wd"])
+            with forward_phase_range(f"layer_{li}_ffn"):
+                up_gate = F.linear(o, lw["wug"])
+                silu_and_mul_inplace(up_gate)
+                x = F.linear(up_gate[:, :inter], lw["wd"])
         x += res
-        return post_layer_forward(x, st, self.final_norm, self.lm_head, eps).tolist()
+        with forward_phase_range("post_lm_head"):
+            return post_layer_forward(x, st, self.final_norm, self.lm_head, eps).tolist()
 
-    def prefill(self, seq_ids: list, prompts: list) -> list:
-        """Run the prompts; returns each one's greedy next token."""
+    def prefill(self, seq_ids: list, prompts: list, ignore_kvcache: bool = False) -> list:
+        """Run the prompts; returns each one's greedy next token.  With
+        ``ignore_kvcache`` the forward leaves the cache untouched
+        (transformer_layer.py:133)."""
         mc, dev = self.mc, self.dev
         lens = [len(p) for p in prompts]
-        st = build_infer_state(seq_ids, [], lens, mc, self.cos, self.sin, dev)
+        st = build_infer_state(seq_ids, [], lens, mc, self.cos, self.sin, dev,
+                               ignore_kvcache=ignore_kvcache)
         d = mc.head_dim
 
         def attention(li, lw, q, k, v):
@@ -134,7 +142,9 @@ class RandomQwen3:
             rmsnorm_inplace(q.view(-1, d), lw["q_norm"], mc.rms_norm_eps)
             rmsnorm_inplace(k.view(-1, d), lw["k_norm"], mc.rms_norm_eps)
             rotary_embedding_inplace(q, k, st)
-            store_kvcache(k, v, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st, li)
+            if not st.ignore_kvcache:
+                with forward_phase_range(f"layer_{li}_store_kvcache"):
+                    store_kvcache(k, v, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st, li)
             return flash_attn_varlen_func(q, k, v, st.prefill_seq_start_locs_with_end,
                                           st.prefill_seq_start_locs_with_end, st.max_prefill_len,
                                           st.max_prefill_len, softmax_scale=st.softmax_scale)
@@ -149,8 +159,10 @@ class RandomQwen3:
 
         def attention(li, lw, q_rows, k, v):
             q = torch.empty(q_rows.shape, dtype=q_rows.dtype, device=dev)  # the prologue's contiguous q
-            qk_norm_rope_store(q_rows, k, v, self.k_cache, self.v_cache, self.block_table,
-                               lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin, q_out=q)
+            with forward_phase_range(f"layer_{li}_store_kvcache"):  # QK-norm + RoPE + store, one launch
+                qk_norm_rope_store(q_rows, k, v, self.k_cache, self.v_cache, self.block_table,
+                                   lw["q_norm"], lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin,
+                                   q_out=q)
             o = torch.empty_like(q)
             if self.check is not None and self.check[0] == li:
                 lse = torch.empty((q.shape[0], hq), dtype=torch.float32, device=dev)
@@ -159,8 +171,9 @@ class RandomQwen3:
                 self.check[1](self, li, q, o, lse, seq_ids, seq_lens)
                 self.check = None
             else:
-                paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
-                                li, o)
+                with forward_phase_range(f"layer_{li}_paged_attention"):
+                    paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
+                                    li, o)
             return o
         return self._forward(st, tokens, attention)
 

@@ -20,7 +20,10 @@ How each function is pinned (see ``tests/test_oracle.py``):
   constant-row closed form ``y = sign(c) * w``.
 * ``rope_cache`` / ``rope`` -- identity at position 0, norm preservation of
   each (x0, x1) pair, equality with a complex-multiplication formulation,
-  ``cos^2 + sin^2 = 1`` and the closed form ``cos(pos)`` for frequency 0.
+  ``cos^2 + sin^2 = 1`` and the closed form ``cos(pos)`` for frequency 0;
+  for dict ``rope_scaling``, equal factors give the number form, and
+  unequal ones split the columns at the stated index, each side equal to
+  the number form of its own factor.
 * ``paged_attention`` -- ``torch.nn.functional.scaled_dot_product_attention``
   (library routine) on the gathered K/V, a pure-Python brute force on tiny
   inputs, the closed forms seq_len=1 -> v_0, identical keys -> mean(V),
@@ -204,17 +207,28 @@ def rmsnorm(x, w, eps):
     return (xf * rstd * w.astype(np.float32)).astype(np.float16)
 
 
-def rope_cache(head_dim: int, theta: float, max_positions: int, scaling: float = 1.0):
-    """cos/sin tables, swiftLLM/swiftllm/worker/model.py:242-252.
+def rope_cache(head_dim: int, theta: float, max_positions: int, scaling=1.0):
+    """cos/sin tables, swiftLLM/swiftllm/worker/model.py:209-252.
 
-    ``inv_freq = 1/theta^(arange(0,d,2)/d)`` and ``t = arange(n)/scaling``
-    in fp32, ``freqs = outer(t, inv_freq)`` in fp32, cos/sin cast to fp16.
-    Returns (cos, sin), each [max_positions, head_dim//2] fp16.
+    Number ``scaling`` (:242-246): ``inv_freq = 1/theta^(arange(0,d,2)/d)``
+    and ``t = arange(n)/scaling`` in fp32, ``freqs = outer(t, inv_freq)``.
+    Dict ``scaling`` (:209-240): frequencies below ``split = int(d/2 * lf /
+    (lf + hf))`` use positions ``t/lf``, the rest ``t/hf`` (lf, hf = the
+    dict's ``low_freq_factor``/``high_freq_factor``, default 1).  cos/sin
+    cast to fp16.  Returns (cos, sin), each [max_positions, head_dim//2].
     """
     exps = np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim)
     inv_freq = (np.float32(1.0) / np.power(np.float32(theta), exps, dtype=np.float32)).astype(np.float32)
-    t = (np.arange(max_positions, dtype=np.float32) / np.float32(scaling)).astype(np.float32)
-    freqs = np.outer(t, inv_freq).astype(np.float32)
+    t = np.arange(max_positions, dtype=np.float32)
+    if isinstance(scaling, dict):
+        lf = np.float32(scaling.get("low_freq_factor", 1.0))
+        hf = np.float32(scaling.get("high_freq_factor", 1.0))
+        split = int((head_dim // 2) * float(lf) / (float(lf) + float(hf)))
+        freqs = np.concatenate([np.outer((t / lf).astype(np.float32), inv_freq[:split]),
+                                np.outer((t / hf).astype(np.float32), inv_freq[split:])], axis=1)
+    else:
+        freqs = np.outer((t / np.float32(scaling)).astype(np.float32), inv_freq)
+    freqs = freqs.astype(np.float32)
     return np.cos(freqs).astype(np.float16), np.sin(freqs).astype(np.float16)
 
 

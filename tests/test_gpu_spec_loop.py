@@ -69,3 +69,46 @@ def test_speculative_loop_shared_weights_accepts(gpu):
     assert results and all(r["ok"] for r in results), [r for r in results if not r["ok"]]
     # a checked draft forward held two-row reconcile groups
     assert any(r["max_q_len"] == 2 and r["rows"] < 5 * 64 for r in results)
+
+
+def test_prefill_ignore_kvcache_leaves_cache(gpu):
+    """A prefill forward with ignore_kvcache writes no cache slot and returns
+    the same tokens (prefill attention reads k/v directly), as the reference's
+    layer skips store_kvcache then (transformer_layer.py:133)."""
+    import torch
+
+    from nebulasd_amd.config import QWEN3_0_6B
+    from nebulasd_amd.spec_loop import RandomQwen3
+
+    m = RandomQwen3(QWEN3_0_6B, [4, 4], gpu, seed=9)
+    prompts = [list(range(100, 140)), list(range(7, 40))]
+    t_ignored = m.prefill([0, 1], prompts, ignore_kvcache=True)
+    torch.cuda.synchronize()
+    assert int(m.k_cache.count_nonzero()) == 0 and int(m.v_cache.count_nonzero()) == 0
+    t_stored = m.prefill([0, 1], prompts)
+    torch.cuda.synchronize()
+    assert t_ignored == t_stored
+    assert int(m.k_cache.count_nonzero()) > 0
+
+
+def test_prologue_refuses_ignore_kvcache_with_decode_rows(gpu):
+    import types
+
+    import torch
+
+    from nebulasd_amd.config import QWEN3_0_6B, EngineConfig, ModelConfig
+    from nebulasd_amd.infer_state import rope_cache
+    from nebulasd_amd.kernels import qk_norm_rope_store
+
+    mc = ModelConfig(QWEN3_0_6B)
+    cos, sin = rope_cache(128, mc.rope_theta, 64, gpu)
+    st = types.SimpleNamespace(num_prefill_seqs=0, num_decoding_seqs=1, ignore_kvcache=True,
+                               seq_ids=torch.zeros(1, dtype=torch.int32, device=gpu),
+                               decoding_seq_lens=torch.full((1,), 5, dtype=torch.int32, device=gpu))
+    kc = torch.zeros((4, mc.num_layers, 8, 16, 128), dtype=torch.float16, device=gpu)
+    q = torch.zeros((1, 16, 128), dtype=torch.float16, device=gpu)
+    k = torch.zeros((1, 8, 128), dtype=torch.float16, device=gpu)
+    with pytest.raises(ValueError, match="ignore_kvcache"):
+        qk_norm_rope_store(q, k, k.clone(), kc, kc.clone(), torch.zeros((1, 4), dtype=torch.int32, device=gpu),
+                           None, None, mc, EngineConfig(max_blocks_per_seq=4), st, 0, cos, sin)
+    assert int(kc.count_nonzero()) == 0

@@ -147,6 +147,51 @@ def test_rope_table_closed_forms():
     np.testing.assert_allclose(cos[4000, 63], math.cos(4000 * f), atol=1e-3)
 
 
+def test_rope_dict_scaling_closed_forms():
+    """Dict rope_scaling (model.py:209-240): equal factors reduce to the
+    number form; unequal ones split the frequency columns at
+    int(d/2 * lf / (lf + hf)), each side equal to the number form of its
+    own factor."""
+    base_c, base_s = oracle.rope_cache(128, 1e6, 3000)
+    c, s = oracle.rope_cache(128, 1e6, 3000, {"low_freq_factor": 1.0, "high_freq_factor": 1.0,
+                                              "factor": 8.0, "rope_type": "llama3"})
+    np.testing.assert_array_equal(c, base_c)
+    np.testing.assert_array_equal(s, base_s)
+    c4, s4 = oracle.rope_cache(128, 1e6, 3000, 4.0)
+    c, s = oracle.rope_cache(128, 1e6, 3000, {"low_freq_factor": 4.0, "high_freq_factor": 4.0})
+    np.testing.assert_array_equal(c, c4)
+    np.testing.assert_array_equal(s, s4)
+    # lf 1, hf 4: split = int(64 * 1 / 5) = 12
+    c, s = oracle.rope_cache(128, 1e6, 3000, {"low_freq_factor": 1.0, "high_freq_factor": 4.0})
+    np.testing.assert_array_equal(c[:, :12], base_c[:, :12])
+    np.testing.assert_array_equal(c[:, 12:], c4[:, 12:])
+    np.testing.assert_array_equal(s[:, :12], base_s[:, :12])
+    np.testing.assert_array_equal(s[:, 12:], s4[:, 12:])
+    # lf 3, hf 1: split = int(64 * 3 / 4) = 48
+    c3, _ = oracle.rope_cache(128, 1e6, 3000, 3.0)
+    c, _ = oracle.rope_cache(128, 1e6, 3000, {"low_freq_factor": 3.0})
+    np.testing.assert_array_equal(c[:, :48], c3[:, :48])
+    np.testing.assert_array_equal(c[:, 48:], base_c[:, 48:])
+    assert not np.array_equal(c[:, 47], base_c[:, 47])  # a planted split one column off would fail
+
+
+def test_product_rope_tables_equal_oracle():
+    """The package's table builder (torch, here on the CPU) gives the oracle's
+    fp16 tables for number and dict scaling."""
+    from nebulasd_amd.config import QWEN3_8B, ModelConfig
+    from nebulasd_amd.infer_state import model_rope_cache, rope_cache
+
+    for scaling in (1.0, 2.5, {"low_freq_factor": 1.0, "high_freq_factor": 4.0, "factor": 8.0}):
+        c, s = rope_cache(128, 1e6, 5000, "cpu", scaling)
+        oc, os_ = oracle.rope_cache(128, 1e6, 5000, scaling)
+        assert np.abs(c.float().numpy() - oc.astype(np.float32)).max() <= 2 ** -10
+        assert np.abs(s.float().numpy() - os_.astype(np.float32)).max() <= 2 ** -10
+    cfg = dict(QWEN3_8B, rope_scaling={"low_freq_factor": 2.0, "high_freq_factor": 2.0})
+    c, _ = model_rope_cache(ModelConfig(cfg), 100, "cpu")
+    oc, _ = oracle.rope_cache(128, QWEN3_8B["rope_theta"], 100, 2.0)
+    assert np.abs(c.float().numpy() - oc.astype(np.float32)).max() <= 2 ** -10
+
+
 def test_rope_identity_norm_and_complex_form():
     rng = np.random.default_rng(4)
     cos, sin = oracle.rope_cache(128, 1e6, 2048)
