@@ -15,10 +15,10 @@
 // The element-wise kernels are HBM-bound (one read and one write of every
 // element) and latency-bound at decode sizes.  lm_head + argmax is a skinny
 // GEMM: the [vocab, hidden] weight (1.24 GB for Qwen3-8B) is streamed once per
-// call at HBM rate by 16x16x32 MFMAs whose other operand (at most 128 rows of
-// x) is staged through LDS; each workgroup folds its logits into one 64-bit
-// key per row, (ordered fp16 value << 32) | ~index, merged with atomicMax so
-// the largest value and then the smallest index win.
+// pass of at most 128 rows of x through an LDS ring by 16x16x32 MFMAs; each
+// wave folds its logits into one 64-bit key per row, (ordered fp16 value <<
+// 32) | ~index, merged with atomicMax so the largest value and then the
+// smallest index win.
 #include <algorithm>
 
 #include "nsd_device.h"
@@ -148,186 +148,220 @@ argmax_rows_kernel(const f16* __restrict__ logits, int64_t vocab, int64_t* token
 
 // ---- lm_head GEMV + argmax -----------------------------------------------
 
-constexpr int kLmK = 128;                                       // k-chunk per step
-constexpr int kLmRowBytes = kLmK * 2 + 16;                      // 272: rows 4 banks apart
-constexpr int kLmMaxRowTiles = 8;                               // <= 128 rows of x per pass
+constexpr int kLmK = 128;  // hidden must be a multiple of this (one ring step of k)
+
+// lm_head GEMV + argmax through an LDS ring (1..128 rows of x per pass).
+//
+// One workgroup per CU streams a balanced range of 16-row vocab tiles, in
+// groups of eight tiles (128 vocab rows), in k steps of 128 (256 bytes of a
+// row).  Four producer waves bring each step's weight chunk (128 rows x
+// 256 B) from memory straight into a slot of a kRgRing-slot LDS ring by
+// global_load_lds_dwordx4, four rows x 256 B per instruction: whole 256-byte
+// runs of a row per instruction, against the 64-byte pieces of 16 rows that
+// a 16x16 MFMA operand loaded into registers gets (measured read rates over
+// the Qwen3-8B lm_head: 5.9 against 5.1 TB/s), with kRgRing - 1 steps in
+// flight.  The 16-byte chunk q of slot row r sits at chunk q ^ (r & 15), so
+// the sixteen rows an operand read touches hit distinct banks.  Consumer
+// wave (rt, h) holds x row tile rt in registers (its own loads, three steps
+// ahead; x is a few hundred KB and stays in L2), multiplies it by vocab
+// tiles [h*TPW, (h+1)*TPW) of the group (A = weight rows, B = x rows, as in
+// the register-staged kernel, so every sum runs in the same k order), folds
+// its logits into one running key per x row at the end of each group, and
+// merges it with one atomicMax at the end.  The two roles never wait on
+// each other's loads: each wave's vmcnt counts its own kind only.
+// Out-of-range weight rows are fetched from one fixed row (an L2 hit) and
+// never used.  Measured on MI355X, Qwen3-8B lm_head: 243 us at 1 row and
+// 253 us at 80 (against 266 / 323 for the register-staged kernel).
+constexpr int kRgTiles = 8;                             // vocab tiles per group
+constexpr int kRgRowBytes = 256;                        // a row's 128 k of one step
+constexpr int kRgRing = 4;                              // ring slots: three steps in flight
+constexpr int kRgSlot = kRgTiles * 16 * kRgRowBytes;    // 32 KB
+constexpr int kRgLds = kRgRing * kRgSlot;
+constexpr int kRgProducers = 4;
+constexpr int kRgInsPerWave = kRgTiles * 16 / 4 / kRgProducers;  // DMA instructions per producer per step
+constexpr int kRgXAhead = 3;                            // steps of x a consumer loads ahead
+constexpr int kRgMaxRowTiles = 8;                       // up to 128 rows of x per pass
+static_assert(kRgLds <= 160 * 1024, "ring fits the CU's LDS");
+static_assert(kRgInsPerWave * (kRgRing - 1) <= 63, "vmcnt range");
+
+// Consumer waves per x row tile: 8, 4, then 1 for 3..8 row tiles (a second
+// wave per tile would load the tile's x again: measured slower at 64-80 rows).
+template <int NRT>
+constexpr int rg_split() { return NRT == 1 ? 8 : NRT == 2 ? 4 : 1; }
+template <int NRT>
+constexpr int rg_threads() { return (kRgProducers + NRT * rg_split<NRT>()) * kWave; }
+
+__device__ inline void rg_dma(uint32_t lds_addr, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(lds_addr), "v"(src) : "memory", "m0");
+}
+template <int N>
+__device__ inline void rg_wait_n() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+// A producer's loads of all but its n most recent steps are complete
+// (0 <= n <= kRgRing - 2).
+template <int N>
+__device__ inline void rg_wait_steps_n() {
+  if constexpr (N * kRgInsPerWave <= 63) rg_wait_n<N * kRgInsPerWave>();
+  else rg_wait_n<0>();
+}
+__device__ inline void rg_wait_steps(int n) {
+  static_assert(kRgRing <= 6, "wait table");
+  switch (n) {
+    case 1: rg_wait_steps_n<1>(); break;
+    case 2: rg_wait_steps_n<2>(); break;
+    case 3: rg_wait_steps_n<3>(); break;
+    case 4: rg_wait_steps_n<4>(); break;
+    default: rg_wait_n<0>(); break;
+  }
+}
 
 template <int NRT>
-constexpr int lm_lds_bytes() { return 2 * NRT * 16 * kLmRowBytes; }
+__global__ void __launch_bounds__(rg_threads<NRT>())
+lm_ring_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden, int64_t vocab,
+               uint64_t* __restrict__ keys) {
+  constexpr int SPLIT = rg_split<NRT>(), TPW = kRgTiles / SPLIT, XR = kRgXAhead + 1;
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool producer = wv < kRgProducers;
+  const int cw = wv - kRgProducers;  // consumer index
+  const int rt = cw % NRT, h = cw / NRT;
+  const int64_t n_tiles = (vocab + 15) / 16;
+  const int64_t t0 = (int64_t)blockIdx.x * n_tiles / gridDim.x;
+  const int64_t t1 = (int64_t)(blockIdx.x + 1) * n_tiles / gridDim.x;
+  const int kch = hidden / 128;
+  const int steps = (int)((t1 - t0 + kRgTiles - 1) / kRgTiles) * kch;
+  const uint32_t ring = (uint32_t)(uintptr_t)lds_raw;
 
-// Workgroup: NW*TPW*16 vocab rows (NW waves x TPW tiles of 16) against
-// NRT*16 rows of x.  MFMA step s of chunk k0 covers k = k0 + 32s .. +31: lane (i, g) loads
-// W row (tile row i) elements 32s + 8g .. +7, so the 4 lanes of a row read
-// 64 contiguous bytes per load instruction (whole 64-byte segments), and the
-// x fragment of row (rt*16 + i) is the same 8 elements from LDS.
-//
-// Pipeline per chunk c: x of chunk c+1 is loaded into registers first, then
-// W of chunk c+1, then chunk c's MFMAs run (x from LDS, W from registers),
-// then the x registers go to the other LDS buffer.  Loads complete in
-// order, so that LDS store waits for the x loads only and the weight loads
-// stay in flight across the MFMAs and the barrier.
-//
-// skinny_mainloop: the wave's weight rows [vbase, vbase + TPW*16) (rows past
-// n_out read as zero) against x rows [0, n_rows) (row stride x_stride) over
-// the k chunks [kc0, kc0 + chunks) of 128; sums accumulate into acc.  Every
-// thread of the workgroup calls it with the same chunk range (it holds
-// barriers).
-template <int NRT, int TPW, int NW, int PD>
-__device__ __forceinline__ void skinny_mainloop(const f16* __restrict__ x, int64_t x_stride,
-                                                const f16* __restrict__ w, int n_rows, int hidden,
-                                                int64_t vbase, int64_t n_out, int kc0, int chunks,
-                                                lds_char* lds, f32x4 (&acc)[TPW][NRT]) {
-  constexpr int kLmThreads = NW * kWave;
-  constexpr int kBuf = NRT * 16 * kLmRowBytes;
-  constexpr int kXRowStep = kLmThreads / (kLmK / 8);      // x rows one pass of the workgroup covers
-  constexpr int kXv = (NRT * 16 + kXRowStep - 1) / kXRowStep;  // 16-byte x vectors per thread per chunk
-  const int lane = threadIdx.x & 63;
-  const int li = lane & 15, lg = lane >> 4;
-  const gbl_u32x4* wp[TPW];
-  bool wok[TPW];
+  // Producer wv: instructions j = wv, wv + kRgProducers, ... of step st, slot rows 4j .. 4j+3.
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int g = st / kch, c = st - g * kch;
+    const uint32_t slot = ring + (uint32_t)((st % kRgRing) * kRgSlot);
 #pragma unroll
-  for (int a = 0; a < TPW; ++a) {
-    const int64_t v = vbase + a * 16 + li;
-    wok[a] = v < n_out;
-    wp[a] = (const gbl_u32x4*)(uintptr_t)(w + (wok[a] ? v : 0) * (int64_t)hidden + (int64_t)kc0 * kLmK + lg * 8);
+    for (int n = 0; n < kRgInsPerWave; ++n) {
+      const int j = wv + kRgProducers * n;
+      const int r = 4 * j + (lane >> 4);
+      const int64_t tile = t0 + (int64_t)g * kRgTiles + (r >> 4);
+      const int64_t v = tile * 16 + (r & 15);
+      const f16* row = w + (tile < t1 && v < vocab ? v : vocab - 1) * (int64_t)hidden;
+      rg_dma(slot + (uint32_t)(4 * j * kRgRowBytes), row + c * 128 + ((lane & 15) ^ (r & 15)) * 8);
+    }
+  };
+  // Consumer: x row tile rt, k = c*128 + 32s + 8*lg .. +7 for s = 0..3 (the B operand of step st).
+  const f16* xrow = x + (int64_t)(rt * 16 + li < n_rows ? rt * 16 + li : n_rows - 1) * hidden + 8 * lg;
+  auto load_x = [&](u32x4 (&xv)[4], int st) __attribute__((always_inline)) {
+    const int c = st % kch;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xv[s] = *reinterpret_cast<const u32x4*>(xrow + c * 128 + 32 * s);
+  };
+
+  if (producer) {
+    int issued = 0;
+    while (issued < steps && issued < kRgRing - 1) issue(issued++);
+    for (int i = 0; i < steps; ++i) {
+      rg_wait_steps(issued - i - 1);            // step i landed (this producer's part) ...
+      asm volatile("s_barrier" ::: "memory");   // ... and the other producers'; step i-1's slot is free
+      if (issued < steps) issue(issued++);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
   }
-  // x vector j of this thread: row xr0 + j*kXRowStep of the chunk, 16-byte
-  // column threadIdx.x % 16.
-  const int xc = threadIdx.x % (kLmK / 8), xr0 = threadIdx.x / (kLmK / 8);
-  const f16* xk = x + (int64_t)kc0 * kLmK;
-  auto load_x = [&](u32x4 (&xv)[kXv], int k0) {
+  // Consumer.  x of step i sits in xv[i % XR].  The main loop runs whole
+  // blocks of XR steps unrolled with no guard, so the register ring keeps
+  // static indices and no register copy waits on a load in flight; every
+  // load is unconditional (steps past the end reload the last step's x).
+  // Steps past the last whole block (only when hidden / 128 is not a
+  // multiple of XR) load their x just before use.
+  f32x4 acc[TPW];
 #pragma unroll
-    for (int j = 0; j < kXv; ++j)
-      if (xr0 + j * kXRowStep < n_rows)
-        xv[j] = *reinterpret_cast<const u32x4*>(xk + (int64_t)(xr0 + j * kXRowStep) * x_stride + k0 + xc * 8);
-  };
-  auto store_x = [&](lds_char* dst, const u32x4 (&xv)[kXv]) {
+  for (int a = 0; a < TPW; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint64_t best = 0;  // this lane's largest key over every group so far (a max folds in any order)
+  auto compute = [&](int i, const u32x4 (&xs)[4]) __attribute__((always_inline)) {
+    const lds_char* sl = (const lds_char*)lds_raw + (i % kRgRing) * kRgSlot;
 #pragma unroll
-    for (int j = 0; j < kXv; ++j)
-      if (xr0 + j * kXRowStep < n_rows)
-        *reinterpret_cast<lds_u32x4*>(dst + (xr0 + j * kXRowStep) * kLmRowBytes + xc * 16) = xv[j];
-  };
-  auto load_w = [&](u32x4 (&wr)[TPW][4], int c) {
+    for (int s = 0; s < 4; ++s) {
+      const int q = (4 * s + lg) ^ li;
+      const f16x8 b = as_h8(xs[s]);
 #pragma unroll
-    for (int a = 0; a < TPW; ++a)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        wr[a][s] = wok[a] ? __builtin_nontemporal_load(wp[a] + c * (kLmK / 8) + s * 4) : u32x4{0, 0, 0, 0};
-  };
-
-  u32x4 xv[kXv];
-  // Register ring of weight chunks: chunk c computes from wr[c % R] while
-  // chunks c+1 .. c+PD load into the others (static indices: the loop is
-  // unrolled by R, so no register moves wait on loads in flight).
-  constexpr int R = PD + 1;
-  u32x4 wr[R][TPW][4];
-  load_x(xv, 0);
-  static_for<PD>([&](auto u) {
-    constexpr int k = decltype(u)::value;
-    if (k < chunks) load_w(wr[k], k);
-  });
-  store_x(lds, xv);
-  __syncthreads();
-  for (int c0 = 0; c0 < chunks; c0 += R) {
-    static_for<R>([&](auto u) {
-      constexpr int k = decltype(u)::value;
-      const int c = c0 + k;
-      if (c < chunks) {
-        const lds_char* cur = lds + (c & 1) * kBuf;
-        lds_char* nxt = lds + ((c + 1) & 1) * kBuf;
-        const bool more = c + 1 < chunks;
-        if (more) load_x(xv, (c + 1) * kLmK);
-        if (c + PD < chunks) load_w(wr[(k + PD) % R], c + PD);
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-          const lds_char* xb = cur + (rt * 16 + li) * kLmRowBytes + lg * 16;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const f16x8 bx = as_h8(*reinterpret_cast<const lds_u32x4*>(xb + s * 64));
-#pragma unroll
-            for (int a = 0; a < TPW; ++a) acc[a][rt] = mfma_k32(as_h8(wr[k][a][s]), bx, acc[a][rt]);
-          }
-        }
-        if (more) store_x(nxt, xv);  // `nxt` was last read in chunk c-1, before the previous barrier
-        __syncthreads();
+      for (int a = 0; a < TPW; ++a) {
+        const int wr = (h * TPW + a) * 16 + li;
+        acc[a] = mfma_k32(as_h8(*reinterpret_cast<const lds_u32x4*>(sl + wr * kRgRowBytes + q * 16)), b, acc[a]);
       }
+    }
+    if ((i + 1) % kch == 0) {  // group end: acc[a][e] is vocab row 4*lg + e of tile a, x row rt*16 + li
+      const int64_t tg = t0 + (int64_t)(i / kch) * kRgTiles + h * TPW;
+#pragma unroll
+      for (int a = 0; a < TPW; ++a) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t v = (tg + a) * 16 + 4 * lg + e;
+          if (tg + a < t1 && v < vocab) best = umax64(best, argmax_key((f16)acc[a][e], (uint32_t)v));
+        }
+        acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  const int full = steps - steps % XR;
+  u32x4 xv[XR][4];
+  static_for<kRgXAhead>([&](auto u) {
+    constexpr int k = decltype(u)::value;
+    load_x(xv[k], k < steps ? k : steps - 1);
+  });
+  for (int i0 = 0; i0 < full; i0 += XR) {
+    static_for<XR>([&](auto u) {
+      constexpr int k = decltype(u)::value;  // step i0 + k uses xv[k]; xv[(k + kRgXAhead) % XR] is refilled
+      const int i = i0 + k;
+      // the refill is issued before the barrier, which the compiler cannot
+      // move loads across: it cannot sink it next to the loads' first use
+      const int nx = i + kRgXAhead;
+      load_x(xv[(k + kRgXAhead) % XR], nx < steps ? nx : steps - 1);
+      asm volatile("s_barrier" ::: "memory");  // step i's weight chunk is in its slot
+      compute(i, xv[k]);
     });
   }
+  for (int i = full; i < steps; ++i) {
+    asm volatile("s_barrier" ::: "memory");
+    u32x4 xs[4];
+    load_x(xs, i);
+    compute(i, xs);
+  }
+  // One key per x row and wave: the four lane groups' rows, then one atomic.
+  best = umax64(best, shfl_xor64(best, 16));
+  best = umax64(best, shfl_xor64(best, 32));
+  const int row = rt * 16 + li;
+  if (lg == 0 && row < n_rows && best)
+    atomicMax(reinterpret_cast<unsigned long long*>(keys + row), (unsigned long long)best);
 }
 
-template <int NRT, int TPW, int NW, int WPE, int PD>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
-lm_head_argmax_kernel(const f16* __restrict__ x, const f16* __restrict__ w, int n_rows, int hidden,
-                      int64_t vocab, uint64_t* __restrict__ keys) {
-  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
-  lds_char* lds = (lds_char*)lds_raw;
-  constexpr int kLmThreads = NW * kWave;
-  __shared__ uint64_t s_best[NW][NRT * 16];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const int64_t vbase = (int64_t)blockIdx.x * (NW * TPW * 16) + wv * (TPW * 16);
-  f32x4 acc[TPW][NRT];
-#pragma unroll
-  for (int a = 0; a < TPW; ++a)
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) acc[a][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  skinny_mainloop<NRT, TPW, NW, PD>(x, hidden, w, n_rows, hidden, vbase, vocab, 0, hidden / kLmK, lds, acc);
-  // acc[a][rt][e]: logit of vocab row vbase + a*16 + 4*lg + e, x row rt*16 + li.
-#pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int a = 0; a < TPW; ++a)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t v = vbase + a * 16 + 4 * lg + e;
-        if (v < vocab) best = umax64(best, argmax_key((f16)acc[a][rt][e], (uint32_t)v));
-      }
-    best = umax64(best, shfl_xor64(best, 16));
-    best = umax64(best, shfl_xor64(best, 32));
-    if (lg == 0) s_best[wv][rt * 16 + li] = best;
-  }
-  __syncthreads();
-  for (int r = threadIdx.x; r < n_rows; r += kLmThreads) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int q = 0; q < NW; ++q) best = umax64(best, s_best[q][r]);
-    if (best) atomicMax(reinterpret_cast<unsigned long long*>(keys + r), (unsigned long long)best);
-  }
+int rg_grid() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
 }
-
-// Per row-tile count (1..8): vocab tiles per wave, waves per workgroup, the
-// waves per SIMD the register budget is fitted to, and the weight prefetch
-// distance in chunks (2 measured slower everywhere: it spills or costs a
-// wave per SIMD).  Measured on MI355X
-// over 1..128 rows of the 151,936 x 4096 and x 1024 lm_heads; every entry
-// compiles without spills.  Two vocab tiles per wave halve the x traffic
-// from LDS per weight byte while the row tiles leave registers for three or
-// four waves per SIMD; beyond five row tiles one tile per wave and
-// eight-wave workgroups (128 vocab rows per x chunk staged) win.
-struct LmCfg { int tpw, nw, wpe, pd; };
-constexpr LmCfg kLmTable[kLmMaxRowTiles] = {{2, 4, 4, 1}, {2, 4, 4, 1}, {2, 4, 4, 1}, {2, 4, 3, 1},
-                                            {2, 4, 3, 1}, {1, 8, 3, 1}, {1, 8, 3, 1}, {1, 8, 3, 1}};
 
 template <int NRT>
-void launch_lm(const f16* x, const f16* w, int rows, int hidden, int64_t vocab, uint64_t* keys, hipStream_t s) {
-  constexpr int TPW = kLmTable[NRT - 1].tpw, NW = kLmTable[NRT - 1].nw, WPE = kLmTable[NRT - 1].wpe;
-  constexpr int PD = kLmTable[NRT - 1].pd;
+void launch_rg(const f16* x, const f16* w, int rows, int hidden, int64_t vocab, uint64_t* keys, hipStream_t s) {
   static bool attr = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_kernel<NRT, TPW, NW, WPE, PD>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, lm_lds_bytes<NRT>()) == hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_ring_kernel<NRT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kRgLds) == hipSuccess;
   }();
   (void)attr;
-  constexpr int kVocabPerWg = NW * TPW * 16;
-  const unsigned grid = (unsigned)((vocab + kVocabPerWg - 1) / kVocabPerWg);
-  hipLaunchKernelGGL((lm_head_argmax_kernel<NRT, TPW, NW, WPE, PD>), dim3(grid), dim3(NW * 64), lm_lds_bytes<NRT>(), s,
-                     x, w, rows, hidden, vocab, keys);
+  const int64_t n_tiles = (vocab + 15) / 16;
+  const unsigned grid = (unsigned)std::min<int64_t>(rg_grid(), n_tiles);
+  hipLaunchKernelGGL(lm_ring_kernel<NRT>, dim3(grid), dim3(rg_threads<NRT>()), kRgLds, s, x, w, rows, hidden, vocab,
+                     keys);
 }
 
 template <int... N>
-void launch_lm_rows(std::integer_sequence<int, N...>, int nrt, const f16* x, const f16* w, int rows, int hidden,
+void launch_rg_rows(std::integer_sequence<int, N...>, int nrt, const f16* x, const f16* w, int rows, int hidden,
                     int64_t vocab, uint64_t* keys, hipStream_t s) {
-  ((nrt == N + 1 ? launch_lm<N + 1>(x, w, rows, hidden, vocab, keys, s) : void()), ...);
+  ((nrt == N + 1 ? launch_rg<N + 1>(x, w, rows, hidden, vocab, keys, s) : void()), ...);
 }
 
 }  // namespace
@@ -394,7 +428,7 @@ extern "C" int nsd_lm_head_argmax(const void* x, const void* lm_head, int64_t n_
     const int rows = (int)std::min<int64_t>(128, n_rows - r0);
     const f16* xr = xp + r0 * hidden;
     uint64_t* kr = keys + r0;
-    launch_lm_rows(std::make_integer_sequence<int, kLmMaxRowTiles>{}, (rows + 15) / 16, xr, wp, rows, (int)hidden,
+    launch_rg_rows(std::make_integer_sequence<int, kRgMaxRowTiles>{}, (rows + 15) / 16, xr, wp, rows, (int)hidden,
                    vocab, kr, s);
     if (int e = launch_status("lm_head_argmax")) return e;
   }
