@@ -20,6 +20,14 @@ thread_local std::string g_last_error;
 // its budget remain for it.
 constexpr int64_t kMinPieceBlocks = 4;
 constexpr int64_t kPieceCostBlocks = 3;
+// Workgroups launch in index order, two per CU: the first half of the grid
+// takes one slot on every CU before the second half arrives, and a CU's
+// earlier workgroup streams a few percent faster than its later one
+// (per-workgroup timelines).  The first half's ranges are cut 1.5% longer,
+// the second half's 1.5% shorter (per mille of the cost cap); the plan stays
+// a function of the forward's rows alone.
+constexpr int64_t kFirstHalfPerMille = 1015;
+constexpr int64_t kSecondHalfPerMille = 985;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -111,7 +119,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   const int64_t total = seg_start[n_segs];
 
   // 3. contiguous block ranges per worker of near-equal cost (the cost model
-  //    above).  The target cost is the smallest one that fits the stream into
+  //    above, weighted by dispatch half).  The target cost is the smallest one that fits the stream into
   //    the workers; it also keeps every segment under kMaxSlotsPerSegment
   //    pieces, every worker under kMaxWorkerPieces pieces and
   //    kMaxWorkerBlocks blocks.
@@ -121,10 +129,12 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
       kMinPieceBlocks, (max_seg + kMaxSlotsPerSegment - 3) / (kMaxSlotsPerSegment - 2));
   // Greedy cut of the stream for a per-worker cost cap; returns the workers used
   // and, if `cuts` is given, each worker's piece boundaries.
+  const int64_t first_half = std::max<int64_t>(1, n_workers) / 2;
   auto cut_stream = [&](int64_t cap, std::vector<int64_t>* cuts) {
     int64_t used = 0, pos = 0, seg_i = 0;
     while (pos < total) {
-      int64_t budget = cap, room = kMaxWorkerBlocks;
+      int64_t budget = cap * (used < first_half ? kFirstHalfPerMille : kSecondHalfPerMille) / 1000;
+      int64_t room = kMaxWorkerBlocks;
       int opened = 0;
       if (cuts) cuts->push_back(-1);  // worker marker
       while (pos < total && opened < kMaxWorkerPieces && room > 0) {

@@ -77,7 +77,9 @@ def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows
 
     words, ws = plan_words(seq_ids, seq_lens, hq, hkv, 128, 16, bt_rows or (max(seq_ids) + 1),
                            stride, workers, max_group_rows)
-    return decode_plan(words), ws
+    p = decode_plan(words)
+    p["requested_workers"] = workers
+    return p, ws
 
 
 def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
@@ -154,17 +156,24 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
     # planner limits: pieces and blocks per worker
     for w in range(p["workers"]):
         assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES and blocks[w] <= MAX_WORKER_BLOCKS
-    # near-equal cost per active worker: blocks plus 3 per piece; only the
-    # last active worker, or one stopped by the piece or block limit, may
-    # fall short
+    # near-equal cost per active worker within each dispatch half (blocks
+    # plus 3 per piece; the first half's cap 1.5% above the second's); only
+    # the last active worker, or one stopped by the piece or block limit,
+    # may fall short
     cost = [sum(int(pieces[pc][2] - pieces[pc][1]) + PIECE_COST for pc in range(ws[w], ws[w + 1]))
             for w in range(p["workers"])]
     active = [w for w in range(p["workers"]) if cost[w] > 0]
-    top = max(cost[w] for w in active)
-    for w in active[:-1]:
-        assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS) or \
-            ws[w + 1] - ws[w] == MAX_WORKER_PIECES or blocks[w] == MAX_WORKER_BLOCKS, \
-            (w, cost[w], top)
+    half = p.get("requested_workers", p["workers"]) // 2
+    for part in ([w for w in active if w < half], [w for w in active if w >= half]):
+        if not part:
+            continue
+        top = max(cost[w] for w in part)
+        for w in part:
+            if w == active[-1]:
+                continue
+            assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS) or \
+                ws[w + 1] - ws[w] == MAX_WORKER_PIECES or blocks[w] == MAX_WORKER_BLOCKS, \
+                (w, cost[w], top)
     assert p["workers"] % 8 == 0
 
 
