@@ -533,11 +533,12 @@ def measure_hostkv(seed: int, reps: int = 6):
 def measure_layer_step(seed: int, reps: int = 20):
     """One whole Qwen3-8B target-verify decoder layer (16 requests x 5 rows,
     contexts U[256, 4096]) in the reference's order
-    (transformer_layer.py:83-201) on this build's kernels, the GEMMs through
-    F.linear (hipBLASLt): fused add-RMSNorm, one fused q/k/v GEMM (the
-    reference runs three; both are timed), the fused prologue reading its rows,
-    paged attention, O GEMM, fused add-RMSNorm, up/gate GEMM, SiLU-and-mul,
-    down GEMM.  Passes of four layers (weights of four distinct layers,
+    (transformer_layer.py:83-201) on this build's kernels, the q/k/v, O and
+    down GEMMs through torch.mm (hipBLASLt): fused add-RMSNorm, one fused
+    q/k/v GEMM (the reference runs three; both are timed), the fused prologue
+    reading its rows, paged attention, O GEMM, fused add-RMSNorm, the up/gate
+    projection with SiLU-and-mul in one pass (also timed as the library GEMM
+    then SiLU-and-mul), down GEMM.  Passes of four layers (weights of four distinct layers,
     1.7 GB, so each layer reads its weights from HBM): the whole layer, the
     GEMMs alone and the rest alone.  Floor: weight bytes + the attention's
     K/V bytes at the device-copy rate.  Timed eagerly (see below)."""
@@ -548,7 +549,7 @@ def measure_layer_step(seed: int, reps: int = 20):
     from nebulasd_amd.config import EngineConfig, ModelConfig
     from nebulasd_amd.infer_state import build_infer_state, rope_cache
     from nebulasd_amd.kernels import (fused_add_rmsnorm_inplace, paged_attention, qk_norm_rope_store,
-                                      silu_and_mul_inplace)
+                                      silu_and_mul_inplace, up_gate_silu_and_mul)
     from nebulasd_amd.workload import make_workload
 
     dev = torch.device("cuda:0")
@@ -584,9 +585,10 @@ def measure_layer_step(seed: int, reps: int = 20):
     ks = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
     vs = qkv[:, (hq + hkv) * d:].view(T, hkv, d)
     ug = torch.empty((T, 2 * I), dtype=torch.float16, device=dev)
+    hh = torch.empty((T, I), dtype=torch.float16, device=dev)
     kv_layer = [mc.num_layers // 2 + i for i in range(n_layers)]
 
-    def layer(i, gemms=True, rest=True, fused_qkv=True):
+    def layer(i, gemms=True, rest=True, fused_qkv=True, fused_ffn=True):
         lw = layers[i]
         if rest:
             fused_add_rmsnorm_inplace(x, res, lw["n_in"], mc.rms_norm_eps)
@@ -608,35 +610,41 @@ def measure_layer_step(seed: int, reps: int = 20):
             torch.mm(o.view(T, -1), lw["wo"].t(), out=oo)
         if rest:
             fused_add_rmsnorm_inplace(oo, res, lw["n_post"], mc.rms_norm_eps)
-        if gemms:
+        if gemms and fused_ffn:  # the up/gate projection and SiLU-and-mul in one kernel
+            up_gate_silu_and_mul(oo, lw["wug"], out=hh)
+        elif gemms:
             torch.mm(oo, lw["wug"].t(), out=ug)
-        if rest:
+        if rest and not fused_ffn:
             silu_and_mul_inplace(ug)
         if gemms:
-            torch.mm(ug[:, :I], lw["wd"].t(), out=x)
+            torch.mm(hh if fused_ffn else ug[:, :I], lw["wd"].t(), out=x)
 
     # Eager, not a graph: captured with the library GEMMs these passes did not
-    # replay to the eager result, so they stay out of graphs.  `reps` passes of four layers are enqueued
-    # back to back between two events; the host's enqueue time is kept too,
-    # so a host-bound figure shows as host_us >= device us.
+    # replay to the eager result, so they stay out of graphs.  `reps` passes
+    # of four layers are enqueued back to back with an event between passes;
+    # the figure is the median pass (a pass the host fell behind in, e.g. when
+    # the process was descheduled, shows as a device gap and is an outlier).
+    # The host's enqueue time is kept too, so a host-bound figure shows as
+    # host_us >= device us.
     stream = torch.cuda.current_stream()
-    out, host = {}, {}
+    out, host, spread = {}, {}, {}
     for name, kw in (("layer", {}), ("gemms_only", {"rest": False}), ("rest_only", {"gemms": False}),
-                     ("layer_three_qkv_gemms", {"fused_qkv": False})):
+                     ("layer_three_qkv_gemms", {"fused_qkv": False}), ("layer_unfused_ffn", {"fused_ffn": False})):
         for i in range(n_layers):
             layer(i, **kw)
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
         t0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(reps):
+        ev[0].record(stream)
+        for r in range(reps):
             for i in range(n_layers):
                 layer(i, **kw)
-        e1.record(stream)
+            ev[r + 1].record(stream)
         host[name] = (time.perf_counter() - t0) * 1e6 / (reps * n_layers)
-        e1.synchronize()
-        out[name] = e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
+        ev[-1].synchronize()
+        per = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / n_layers for r in range(reps)])
+        out[name] = float(np.median(per))
+        spread[name] = [float(np.percentile(per, q)) for q in (10, 50, 90)]
     kv_bytes = w.algorithmic_bytes()
     copy = getattr(measure_layer_step, "copy_gbps", None)
     floor = (weight_bytes + (kv_bytes or 0)) / (copy * 1e3) if copy and kv_bytes else None
@@ -645,12 +653,16 @@ def measure_layer_step(seed: int, reps: int = 20):
     return {"workload": "layer_step_target_verify", "kind": "whole_layer", "rows": T,
             "us_per_layer": out["layer"], "gemms_only_us": out["gemms_only"], "rest_only_us": out["rest_only"],
             "us_per_layer_three_qkv_gemms": out["layer_three_qkv_gemms"],
+            "us_per_layer_unfused_ffn": out["layer_unfused_ffn"],
+            "us_per_layer_p10_p50_p90": spread,
             "host_enqueue_us_per_layer": host,
             "weight_bytes_per_layer": weight_bytes, "kv_bytes_per_layer": kv_bytes,
             "floor_us_at_copy_rate": floor,
-            "note": "GEMMs through torch.mm (hipBLASLt): one fused q/k/v projection read by the strided prologue "
-                    "(us_per_layer_three_qkv_gemms: the reference's three); the rest is this build's kernels; eager "
-                    "passes of four layers with distinct weights"}
+            "note": "q/k/v, O and down GEMMs through torch.mm (hipBLASLt): one fused q/k/v projection read by the "
+                    "strided prologue (us_per_layer_three_qkv_gemms: the reference's three); the up/gate projection "
+                    "and SiLU-and-mul in one kernel of this build, counted with the GEMMs (us_per_layer_unfused_ffn: "
+                    "the library up/gate GEMM then this build's SiLU-and-mul); the rest is this build's kernels; "
+                    "eager passes of four layers with distinct weights"}
 
 
 def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
@@ -662,6 +674,12 @@ def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
       the target-verify batch (16 requests x 5 rows, Qwen3-8B lm_head
       151,936 x 4096) and the draft batch (64 rows, Qwen3-0.6B 151,936 x 1024);
       algorithmic bytes = the lm_head weight, read once;
+    * the FFN's up/gate projection + SiLU-and-mul in one pass
+      (transformer_layer.py:199-200) at the verify batch (80 rows, Qwen3-8B
+      12,288 x 2 x 4096) and the draft batch (64 rows, Qwen3-0.6B
+      3072 x 2 x 1024), beside the library GEMM then this build's
+      SiLU-and-mul and the reference's torch formulation; algorithmic bytes =
+      the stacked weight, read once;
     * fused add-RMSNorm (rmsnorm.py:39-89) and SiLU-and-mul
       (silu_and_mul.py:5-34) at the verify batch (80 tokens) and a prefill
       chunk (8,192 tokens), Qwen3-8B widths; algorithmic bytes = every element
@@ -677,7 +695,8 @@ def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
     import torch
     import torch.nn.functional as F
 
-    from nebulasd_amd.kernels import fused_add_rmsnorm_inplace, lm_head_argmax, silu_and_mul_inplace
+    from nebulasd_amd.kernels import (fused_add_rmsnorm_inplace, lm_head_argmax, silu_and_mul_inplace,
+                                      up_gate_silu_and_mul)
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -739,6 +758,43 @@ def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
                      "roofline": {"bound": "hbm", "achieved": nbytes / ours / 1e3, "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": nbytes / ours / 1e3 / HBM_PEAK_GBPS}}
         del x, w
+    torch.cuda.empty_cache()
+    for name, rows, hidden, inter in (("up_gate_silu_and_mul_target_verify", 80, 4096, 12288),
+                                      ("up_gate_silu_and_mul_draft_decode", 64, 1024, 3072)):
+        # weight sets used in turn, together past the 256 MB MALL, so every
+        # call reads its weight from HBM
+        nbytes = 2 * inter * hidden * 2
+        n_sets = max(2, -(-600_000_000 // nbytes))
+        ws = [(torch.randn(2 * inter, hidden, device=dev, generator=g) * 0.03).half() for _ in range(n_sets)]
+        x = torch.randn(rows, hidden, device=dev, generator=g).half()
+        h = torch.empty(rows, inter, device=dev, dtype=torch.float16)
+        wturn = itertools.cycle(range(n_sets))
+
+        def ours_ug():
+            up_gate_silu_and_mul(x, ws[next(wturn)], out=h)
+
+        def lib_ug():  # the library GEMM, then this build's SiLU-and-mul
+            ug = F.linear(x, ws[next(wturn)])
+            silu_and_mul_inplace(ug)
+
+        def ref_ug():  # the reference's formulation in torch
+            ug = F.linear(x, ws[next(wturn)])
+            ug[:, :inter] = ug[:, :inter] * F.silu(ug[:, inter:].float()).half()
+        ours = timed(ours_ug)
+        lib = timed(lib_ug)
+        ref = timed(ref_ug)
+        ours_graph = graph_us(ours_ug, calls=n_sets)
+        ug = F.linear(x, ws[0])
+        silu_and_mul_inplace(ug)
+        diff = float((up_gate_silu_and_mul(x, ws[0]).float() - ug[:, :inter].float()).abs().max().item())
+        out[name] = {"rows": rows, "hidden": hidden, "inter": inter, "us_per_call": ours,
+                     "us_per_call_graph": ours_graph, "library_gemm_then_silu_us_per_call": lib,
+                     "reference_us_per_call": ref, "speedup_vs_reference": ref / ours,
+                     "speedup_vs_library_gemm_then_silu": lib / ours, "hbm_gbps": nbytes / ours_graph / 1e3,
+                     "max_abs_diff_vs_library_gemm_then_silu": diff,
+                     "roofline": {"bound": "hbm", "achieved": nbytes / ours_graph / 1e3, "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": nbytes / ours_graph / 1e3 / HBM_PEAK_GBPS}}
+        del ws, x, h, ug
     torch.cuda.empty_cache()
     hidden, inter = 4096, 12288
     for tokens in (80, 8192):
@@ -1136,19 +1192,26 @@ def main():
     if args.layer_step:
         measure_layer_step.copy_gbps = copy_gbps
         r2 = measure_layer_step(args.seed)
-        print("# target verify layer: %.1f us (three q/k/v GEMMs %.1f; GEMMs alone %.1f, rest alone %.1f; floor %s us)"
-              % (r2["us_per_layer"], r2["us_per_layer_three_qkv_gemms"], r2["gemms_only_us"], r2["rest_only_us"],
+        print("# target verify layer: %.1f us (three q/k/v GEMMs %.1f; library up/gate GEMM + SiLU-mul %.1f; "
+              "GEMMs alone %.1f, rest alone %.1f; floor %s us)"
+              % (r2["us_per_layer"], r2["us_per_layer_three_qkv_gemms"], r2["us_per_layer_unfused_ffn"],
+                 r2["gemms_only_us"], r2["rest_only_us"],
                  "%.1f" % r2["floor_us_at_copy_rate"] if r2["floor_us_at_copy_rate"] else "n/a"),
               file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.layer_rest:
         r2 = measure_layer_rest(args.seed, cpu_seconds=args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
         print("# rest of layer: lm_head+argmax verify %.1f us (reference %.1f), draft %.1f us (reference %.1f); "
+              "up/gate+silu-mul verify %.1f us (library GEMM + silu-mul %.1f), draft %.1f us (%.1f); "
               "add-rmsnorm 8192 tok %.1f us (reference %.1f); silu-mul 8192 tok %.1f us (reference %.1f)" % (
                   r2["lm_head_argmax_target_verify"]["us_per_call"],
                   r2["lm_head_argmax_target_verify"]["reference_us_per_call"],
                   r2["lm_head_argmax_draft_decode"]["us_per_call"],
                   r2["lm_head_argmax_draft_decode"]["reference_us_per_call"],
+                  r2["up_gate_silu_and_mul_target_verify"]["us_per_call"],
+                  r2["up_gate_silu_and_mul_target_verify"]["library_gemm_then_silu_us_per_call"],
+                  r2["up_gate_silu_and_mul_draft_decode"]["us_per_call"],
+                  r2["up_gate_silu_and_mul_draft_decode"]["library_gemm_then_silu_us_per_call"],
                   r2["fused_add_rmsnorm_8192_tokens"]["us_per_call"],
                   r2["fused_add_rmsnorm_8192_tokens"]["reference_us_per_call"],
                   r2["silu_and_mul_8192_tokens"]["us_per_call"],

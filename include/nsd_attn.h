@@ -371,6 +371,22 @@ int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void* weight, i
 int nsd_silu_and_mul_inplace(void* x, int64_t n_tokens, int64_t inter_dim, void* stream);
 
 /*
+ * nsd_up_gate_silu_and_mul: the layer's up/gate projection followed by
+ * silu_and_mul (swiftLLM/swiftllm/worker/layers/transformer_layer.py:199-200:
+ * `up_gate_proj = linear(o, up_gate_proj)`, then `silu_and_mul_inplace`)
+ * in one pass over the weight, without the [n_rows, 2 * inter] product:
+ * y[r][j] = fp16(up * fp16(g / (1 + exp(-g)))) with up = fp16(x[r] . W[j])
+ * and g = fp16(x[r] . W[inter + j]) (fp32 sums), W = up_gate [2 * inter,
+ * hidden] row-major (up rows, then gate rows), x [n_rows, hidden], y
+ * [n_rows, inter], fp16.  hidden a multiple of 128, inter a multiple of 16,
+ * pointers 16-byte aligned.  Rows are processed in passes of 128, each
+ * reading W once: meant for decode and verify batches (a library GEMM is
+ * faster at prefill sizes).
+ */
+int nsd_up_gate_silu_and_mul(const void* x, const void* up_gate, void* y, int64_t n_rows,
+                             int64_t hidden, int64_t inter, void* stream);
+
+/*
  * nsd_lm_head_argmax: the post-layer's logits and argmax
  * (swiftLLM/swiftllm/worker/layers/post_layer.py:70-71,
  * `argmax(linear(last_input, lm_head), dim=1)`) without the logits tensor:

@@ -364,6 +364,189 @@ void launch_rg_rows(std::integer_sequence<int, N...>, int nrt, const f16* x, con
   ((nrt == N + 1 ? launch_rg<N + 1>(x, w, rows, hidden, vocab, keys, s) : void()), ...);
 }
 
+// ---- up/gate projection + SiLU·mul ----------------------------------------
+//
+// y[r][j] = fp16(up * fp16(silu(gate))) with up = fp16(x[r] . W[j]) and
+// gate = fp16(x[r] . W[I + j]), W the stacked [2I, hidden] up_gate_proj
+// weight: the reference's up/gate GEMM followed by silu_and_mul, with the
+// same two fp16 roundings, without writing the [rows, 2I] product.  Same
+// main loop as the lm_head kernel: one workgroup per CU owns a balanced
+// range of 16-column output tiles, taken TO at a time; a group's ring slot
+// holds the TO up tiles then the TO gate tiles (32*TO weight rows x 256 B of
+// one k step of 128), brought in by four producer waves with
+// global_load_lds_dwordx4; one consumer wave per 16-row tile of x holds its
+// x rows in registers, loaded kUgXAhead steps ahead.  An up tile and its gate
+// tile land in the same lane layout, so the SiLU·mul runs on the
+// accumulators.  Ring depth grows as the slot shrinks, so every shape keeps
+// about 100 KB in flight per CU.
+template <int TO>
+constexpr int ug_ring() { return TO == 1 ? 16 : TO == 2 ? 8 : TO == 3 ? 6 : TO == 4 ? 4 : 3; }
+template <int TO>
+constexpr int ug_xahead() { return TO == 1 ? 5 : TO == 2 ? 4 : 3; }
+template <int TO>
+constexpr int ug_slot() { return 2 * TO * 16 * kRgRowBytes; }
+template <int TO>
+constexpr int ug_lds() { return ug_ring<TO>() * ug_slot<TO>(); }
+constexpr int kUgMaxTiles = 6;  // output tiles per group (12 weight tiles, a 48 KB slot)
+
+// All but this producer's n most recent DMA instructions are complete.
+__device__ inline void ug_wait(int n) {
+#define NSD_UG_CASE(k) \
+  case k:              \
+    rg_wait_n<k>();    \
+    break;
+  switch (n) {
+    NSD_UG_CASE(0) NSD_UG_CASE(1) NSD_UG_CASE(2) NSD_UG_CASE(3) NSD_UG_CASE(4) NSD_UG_CASE(5) NSD_UG_CASE(6)
+    NSD_UG_CASE(7) NSD_UG_CASE(8) NSD_UG_CASE(9) NSD_UG_CASE(10) NSD_UG_CASE(11) NSD_UG_CASE(12)
+    NSD_UG_CASE(13) NSD_UG_CASE(14) NSD_UG_CASE(15) NSD_UG_CASE(16) NSD_UG_CASE(17) NSD_UG_CASE(18)
+    NSD_UG_CASE(19) NSD_UG_CASE(20) NSD_UG_CASE(21) NSD_UG_CASE(22) NSD_UG_CASE(23) NSD_UG_CASE(24)
+    NSD_UG_CASE(25) NSD_UG_CASE(26) NSD_UG_CASE(27) NSD_UG_CASE(28) NSD_UG_CASE(29) NSD_UG_CASE(30)
+    default: rg_wait_n<0>(); break;
+  }
+#undef NSD_UG_CASE
+}
+
+template <int NRT, int TO>
+__global__ void __launch_bounds__((kRgProducers + NRT) * kWave)
+up_gate_silu_kernel(const f16* __restrict__ x, const f16* __restrict__ w, f16* __restrict__ y, int n_rows,
+                    int hidden, int inter) {
+  constexpr int G = 2 * TO, RING = ug_ring<TO>(), SLOT = ug_slot<TO>(), XA = ug_xahead<TO>(), XR = XA + 1;
+  static_assert((RING - 1) * G <= 30, "wait table");
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n_tiles = inter / 16;
+  const int t0 = (int)((int64_t)blockIdx.x * n_tiles / gridDim.x);
+  const int t1 = (int)((int64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
+  const int kch = hidden / 128;
+  const int steps = (t1 - t0 + TO - 1) / TO * kch;
+  const uint32_t ring = (uint32_t)(uintptr_t)lds_raw;
+
+  if (wv < kRgProducers) {
+    // Producer wv: instructions j = wv, wv + 4, ... of a step, slot rows
+    // 4j .. 4j+3; slot row r < 16*TO is up tile r/16 of the group, the rest
+    // the same gate tiles.  Tiles past the range fetch the range's last one.
+    auto issue = [&](int st) __attribute__((always_inline)) {
+      const int g = st / kch, c = st - g * kch;
+      const uint32_t slot = ring + (uint32_t)((st % RING) * SLOT);
+#pragma unroll
+      for (int n = 0; n < G; ++n) {
+        const int j = wv + kRgProducers * n;
+        const int r = 4 * j + (lane >> 4);
+        const int half = r >= 16 * TO, rr = r - half * 16 * TO;
+        const int tile = t0 + g * TO + (rr >> 4);
+        const int64_t v = (int64_t)half * inter + (int64_t)(tile < t1 ? tile : t1 - 1) * 16 + (rr & 15);
+        rg_dma(slot + (uint32_t)(4 * j * kRgRowBytes), w + v * hidden + c * 128 + ((lane & 15) ^ (r & 15)) * 8);
+      }
+    };
+    int issued = 0;
+    while (issued < steps && issued < RING - 1) issue(issued++);
+    for (int i = 0; i < steps; ++i) {
+      ug_wait((issued - i - 1) * G);            // step i landed (this producer's part) ...
+      asm volatile("s_barrier" ::: "memory");   // ... and the others'; step i-1's slot is free
+      if (issued < steps) issue(issued++);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  // Consumer: x row tile rt, k = c*128 + 32s + 8*lg .. +7 (the B operand).
+  const int rt = wv - kRgProducers;
+  const int row = rt * 16 + li;
+  const f16* xrow = x + (int64_t)(row < n_rows ? row : n_rows - 1) * hidden + 8 * lg;
+  auto load_x = [&](u32x4 (&xv)[4], int st) __attribute__((always_inline)) {
+    const int c = st % kch;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xv[s] = *reinterpret_cast<const u32x4*>(xrow + c * 128 + 32 * s);
+  };
+  f32x4 acc[G];
+#pragma unroll
+  for (int a = 0; a < G; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int i, const u32x4 (&xs)[4]) __attribute__((always_inline)) {
+    const lds_char* sl = (const lds_char*)lds_raw + (i % RING) * SLOT;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int q = (4 * s + lg) ^ li;
+      const f16x8 b = as_h8(xs[s]);
+#pragma unroll
+      for (int a = 0; a < G; ++a)
+        acc[a] = mfma_k32(as_h8(*reinterpret_cast<const lds_u32x4*>(sl + (a * 16 + li) * kRgRowBytes + q * 16)), b,
+                          acc[a]);
+    }
+    if ((i + 1) % kch == 0) {  // group end: acc[a][e] is column 4*lg + e of tile a, x row `row`
+      const int tg = t0 + (i / kch) * TO;
+#pragma unroll
+      for (int a = 0; a < TO; ++a) {
+        if (tg + a < t1 && row < n_rows) {
+          f16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16 up = (f16)acc[a][e];
+            const float g = (float)(f16)acc[TO + a][e];
+            const f16 sg = (f16)(g / (1.f + expf(-g)));
+            o[e] = (f16)((float)up * (float)sg);
+          }
+          *reinterpret_cast<f16x4*>(y + (int64_t)row * inter + (tg + a) * 16 + 4 * lg) = o;
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < G; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // x of step i sits in xv[i % XR]; the main loop runs whole blocks of XR
+  // steps with no guard (static register indices, unconditional loads).
+  const int full = steps - steps % XR;
+  u32x4 xv[XR][4];
+  static_for<XA>([&](auto u) {
+    constexpr int k = decltype(u)::value;
+    load_x(xv[k], k < steps ? k : steps - 1);
+  });
+  for (int i0 = 0; i0 < full; i0 += XR) {
+    static_for<XR>([&](auto u) {
+      constexpr int k = decltype(u)::value;
+      const int i = i0 + k;
+      const int nx = i + XA;
+      load_x(xv[(k + XA) % XR], nx < steps ? nx : steps - 1);
+      asm volatile("s_barrier" ::: "memory");  // step i's weight chunk is in its slot
+      compute(i, xv[k]);
+    });
+  }
+  for (int i = full; i < steps; ++i) {
+    asm volatile("s_barrier" ::: "memory");
+    u32x4 xs[4];
+    load_x(xs, i);
+    compute(i, xs);
+  }
+}
+
+template <int NRT, int TO>
+void launch_ug(const f16* x, const f16* w, f16* y, int rows, int hidden, int inter, int grid, hipStream_t s) {
+  static bool attr = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&up_gate_silu_kernel<NRT, TO>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, ug_lds<TO>()) == hipSuccess;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL((up_gate_silu_kernel<NRT, TO>), dim3(grid), dim3((kRgProducers + NRT) * kWave), ug_lds<TO>(), s,
+                     x, w, y, rows, hidden, inter);
+}
+
+template <int NRT>
+void launch_ug_to(int to, const f16* x, const f16* w, f16* y, int rows, int hidden, int inter, int grid,
+                  hipStream_t s) {
+  switch (to) {
+    case 1: launch_ug<NRT, 1>(x, w, y, rows, hidden, inter, grid, s); break;
+    case 2: launch_ug<NRT, 2>(x, w, y, rows, hidden, inter, grid, s); break;
+    case 3: launch_ug<NRT, 3>(x, w, y, rows, hidden, inter, grid, s); break;
+    case 4: launch_ug<NRT, 4>(x, w, y, rows, hidden, inter, grid, s); break;
+    default: launch_ug<NRT, 6>(x, w, y, rows, hidden, inter, grid, s); break;
+  }
+}
+
+template <int... N>
+void launch_ug_rows(std::integer_sequence<int, N...>, int nrt, int to, const f16* x, const f16* w, f16* y, int rows,
+                    int hidden, int inter, int grid, hipStream_t s) {
+  ((nrt == N + 1 ? launch_ug_to<N + 1>(to, x, w, y, rows, hidden, inter, grid, s) : void()), ...);
+}
+
 }  // namespace
 }  // namespace nsd
 
@@ -435,6 +618,35 @@ extern "C" int nsd_lm_head_argmax(const void* x, const void* lm_head, int64_t n_
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)((n_rows + 255) / 256)), dim3(256), 0, s, keys, tokens,
                      (int)n_rows);
   return launch_status("lm_head_argmax finalize");
+}
+
+extern "C" int nsd_up_gate_silu_and_mul(const void* x, const void* up_gate, void* y, int64_t n_rows, int64_t hidden,
+                                        int64_t inter, void* stream) {
+  if (n_rows < 0 || hidden <= 0 || inter <= 0) return fail(NSD_ERR_INVALID, "up_gate_silu_and_mul: bad shape");
+  if (n_rows == 0) return NSD_OK;
+  if (!x || !up_gate || !y) return fail(NSD_ERR_INVALID, "up_gate_silu_and_mul: null pointer");
+  if (hidden % kLmK || hidden > INT32_MAX / 2)
+    return fail(NSD_ERR_UNSUPPORTED, "up_gate_silu_and_mul: hidden=%lld (need a multiple of %d)", (long long)hidden,
+                kLmK);
+  if (inter % 16 || inter > INT32_MAX / 2)
+    return fail(NSD_ERR_UNSUPPORTED, "up_gate_silu_and_mul: inter=%lld (need a multiple of 16)", (long long)inter);
+  if (!aligned16(x) || !aligned16(up_gate) || !aligned16(y))
+    return fail(NSD_ERR_UNSUPPORTED, "up_gate_silu_and_mul: pointers must be 16-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  const int n_tiles = (int)(inter / 16);
+  const int grid = std::min(rg_grid(), n_tiles);
+  const int per = (n_tiles + grid - 1) / grid;  // output tiles of the busiest workgroup
+  const int to = per <= 4 ? per : per <= 6 ? 6 : kUgMaxTiles;
+  const f16* xp = static_cast<const f16*>(x);
+  // Rows in passes of at most 128 (each pass streams the weight once).
+  for (int64_t r0 = 0; r0 < n_rows; r0 += 128) {
+    const int rows = (int)std::min<int64_t>(128, n_rows - r0);
+    launch_ug_rows(std::make_integer_sequence<int, kRgMaxRowTiles>{}, (rows + 15) / 16, to, xp + r0 * hidden,
+                   static_cast<const f16*>(up_gate), static_cast<f16*>(y) + r0 * inter, rows, (int)hidden, (int)inter,
+                   grid, s);
+    if (int e = launch_status("up_gate_silu_and_mul")) return e;
+  }
+  return NSD_OK;
 }
 
 extern "C" int nsd_argmax_rows(const void* logits, int64_t n_rows, int64_t vocab, int64_t* tokens, void* stream) {

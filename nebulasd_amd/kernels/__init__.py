@@ -9,10 +9,11 @@ from .prefill_attn import flash_attn_varlen_func, prefill_attention
 from .prologue import qk_norm_rope_store
 from .rmsnorm import fused_add_rmsnorm_inplace, rmsnorm_inplace
 from .rotary_emb import rotary_embedding_inplace
-from .silu_and_mul import silu_and_mul_inplace
+from .silu_and_mul import FUSED_UP_GATE_MAX_ROWS, silu_and_mul_inplace, up_gate_silu_and_mul
 
 __all__ = ["paged_attention", "store_kvcache", "rotary_embedding_inplace", "rmsnorm_inplace",
            "qk_norm_rope_store", "flash_attn_varlen_func", "prefill_attention",
            "set_block_table_and_num_seq_alloc_blocks", "unset_block_table_and_num_seq_alloc_blocks",
            "gather_allocated_blocks_and_unset", "write_block_table_ranges", "fused_add_rmsnorm_inplace",
-           "silu_and_mul_inplace", "lm_head_argmax", "argmax_rows", "post_layer_forward"]
+           "silu_and_mul_inplace", "up_gate_silu_and_mul", "FUSED_UP_GATE_MAX_ROWS", "lm_head_argmax",
+           "argmax_rows", "post_layer_forward"]

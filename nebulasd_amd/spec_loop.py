@@ -14,12 +14,14 @@ this package's gfx950 kernels:
 * the rest of the layer in the reference's order
   (transformer_layer.py:83-201, model.py:266-301): the residual buffer with
   ``fused_add_rmsnorm_inplace`` before attention and before the FFN, the
-  stacked up/gate GEMM with ``silu_and_mul_inplace``, one fused q/k/v GEMM
-  (the reference runs three) whose row slices the prologue reads, and the post-layer's
-  last-token norm with the fused lm_head + argmax (``post_layer_forward``);
-  the GEMMs are library GEMMs through ``F.linear`` as in the reference
-  (kernels/linear.py:3-12).  Weights are random (no checkpoints are
-  available offline).
+  stacked up/gate projection and SiLU-and-mul in one pass over the weight
+  (``up_gate_silu_and_mul``) for decode and verify batches (the library GEMM
+  and ``silu_and_mul_inplace`` for prompts), one fused q/k/v GEMM (the
+  reference runs three) whose row slices the prologue reads, and the
+  post-layer's last-token norm with the fused lm_head + argmax
+  (``post_layer_forward``); the other GEMMs are library GEMMs through
+  ``F.linear`` as in the reference (kernels/linear.py:3-12).  Weights are
+  random (no checkpoints are available offline).
 
 The loop is NebulaSD's linear speculation: the draft proposes ``depth``
 tokens with single-token decode steps (nebulasd workers/draft/backend.py:52-70);
@@ -49,9 +51,9 @@ import torch.nn.functional as F
 
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from .infer_state import build_infer_state, model_rope_cache
-from .kernels import (flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention, post_layer_forward,
-                      qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace, silu_and_mul_inplace,
-                      store_kvcache)
+from .kernels import (FUSED_UP_GATE_MAX_ROWS, flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention,
+                      post_layer_forward, qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace,
+                      silu_and_mul_inplace, store_kvcache, up_gate_silu_and_mul)
 from .phases import forward_phase_range
 from .speculative import compute_greedy_acceptance
 
@@ -120,9 +122,13 @@ class RandomQwen3:
                 o = F.linear(o.view(x.shape[0], -1), lw["wo"])
             fused_add_rmsnorm_inplace(o, res, lw["n_post"], eps)
             with forward_phase_range(f"layer_{li}_ffn"):
-                up_gate = F.linear(o, lw["wug"])
-                silu_and_mul_inplace(up_gate)
-                x = F.linear(up_gate[:, :inter], lw["wd"])
+                if o.shape[0] <= FUSED_UP_GATE_MAX_ROWS:  # decode / verify batches: one pass over the weight
+                    h = up_gate_silu_and_mul(o, lw["wug"])
+                else:
+                    up_gate = F.linear(o, lw["wug"])
+                    silu_and_mul_inplace(up_gate)
+                    h = up_gate[:, :inter]
+                x = F.linear(h, lw["wd"])
         x += res
         with forward_phase_range("post_lm_head"):
             return post_layer_forward(x, st, self.final_norm, self.lm_head, eps).tolist()

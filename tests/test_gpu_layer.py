@@ -1,10 +1,14 @@
 """GPU parity of the rest-of-layer kernels (fused add-RMSNorm, SiLU-and-mul,
-lm_head + argmax, argmax) against the numpy oracle, and against the
-reference's own torch formulation on the same GPU.
+the fused up/gate projection + SiLU-and-mul, lm_head + argmax, argmax)
+against the numpy oracle, and against the reference's own torch
+formulation on the same GPU.
 
 Every case prints its name first (pytest -v) so a failing GPU step is named.
 Tolerances: residual and argmax over given logits bit-exact; normalised and
-activated values within 1e-3 (fp16 output, one rounding apart); lm_head
+activated values within 1e-3 (fp16 output, one rounding apart); the fused
+up/gate + SiLU-and-mul within rtol 4e-3 / atol 2e-3 and at least 90% bit-equal
+(its up or gate value may sit one fp16 rounding from the float64 sum's, which
+the SiLU and the product carry); lm_head
 argmax equal to the float64 reference's except where the two candidates'
 float64 logits are within 2e-3 of each other (accumulation order decides a
 near tie).
@@ -19,7 +23,7 @@ import torch.nn.functional as F
 
 import oracle
 from nebulasd_amd import _lib
-from nebulasd_amd.kernels import fused_add_rmsnorm_inplace, silu_and_mul_inplace
+from nebulasd_amd.kernels import fused_add_rmsnorm_inplace, silu_and_mul_inplace, up_gate_silu_and_mul
 from nebulasd_amd.kernels.post_layer import (argmax_rows, last_token_indices, lm_head_argmax,
                                              post_layer_forward)
 
@@ -66,6 +70,53 @@ def test_silu_and_mul_matches_oracle(gpu, rows, inter):
     exact = np.mean(got[:, :inter] == want)
     assert exact > 0.99
     print(f"silu_and_mul {rows}x{inter}: exact {exact:.4f}", flush=True)
+
+
+@pytest.mark.parametrize("rows,hidden,inter", [(1, 4096, 12288), (80, 4096, 12288), (64, 1024, 3072),
+                                               (129, 1024, 3072), (33, 256, 4800), (16, 128, 16),
+                                               (20, 512, 28672)])
+def test_up_gate_silu_and_mul_matches_oracle(gpu, rows, hidden, inter):
+    """The FFN's up/gate GEMM + SiLU-and-mul in one pass against the oracle's
+    float64 GEMM rounded to fp16 then its SiLU-and-mul (transformer_layer.py:
+    199-200), and against the library GEMM then this build's SiLU-and-mul.
+    Shapes: the Qwen3-8B verify and Qwen3-0.6B draft batches, one row, two
+    passes of rows (129), output tiles not a multiple of the CU count (300),
+    one tile, and more tiles per workgroup than one group holds (7 of 6).
+    Rows past the output are never written."""
+    x = _randn(gpu, rows, hidden, seed=11)
+    w = _randn(gpu, 2 * inter, hidden, seed=12, scale=0.03)
+    big = torch.full((rows + 1, inter), 7.0, dtype=torch.float16, device=gpu)
+    out = up_gate_silu_and_mul(x, w, out=big[:rows])
+    torch.cuda.synchronize()
+    assert out.data_ptr() == big.data_ptr()
+    assert bool((big[rows] == 7.0).all()), "a row past the output was written"
+    got = out.cpu().numpy().astype(np.float64)
+    want = oracle.silu_and_mul(oracle.lm_head_logits(x.cpu().numpy(), w.cpu().numpy())).astype(np.float64)
+    # fp32 against float64 sums: an up or gate value one fp16 rounding apart
+    np.testing.assert_allclose(got, want, rtol=4e-3, atol=2e-3)
+    exact = float(np.mean(got == want))
+    assert exact > 0.9
+    ug = F.linear(x, w)
+    silu_and_mul_inplace(ug)
+    lib = ug[:, :inter].float().cpu().numpy()
+    np.testing.assert_allclose(got, lib, rtol=4e-3, atol=2e-3)
+    print(f"up_gate_silu_and_mul {rows}x{hidden}x{inter}: exact vs oracle {exact:.4f}, "
+          f"vs library path {float(np.mean(got == lib)):.4f}", flush=True)
+
+
+def test_up_gate_silu_and_mul_rejects_bad_shapes(gpu):
+    x = torch.zeros(2, 100, dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.NativeLibraryError, match="hidden=100"):
+        up_gate_silu_and_mul(x, torch.zeros(32, 100, dtype=torch.float16, device=gpu))
+    x = torch.zeros(2, 128, dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.NativeLibraryError, match="inter=24"):
+        up_gate_silu_and_mul(x, torch.zeros(48, 128, dtype=torch.float16, device=gpu))
+    with pytest.raises(ValueError):
+        up_gate_silu_and_mul(x, torch.zeros(33, 128, dtype=torch.float16, device=gpu))
+    with pytest.raises(ValueError):
+        up_gate_silu_and_mul(x, torch.zeros(32, 128, dtype=torch.float16, device=gpu),
+                             out=torch.zeros(2, 15, dtype=torch.float16, device=gpu))
+    assert up_gate_silu_and_mul(x[:0], torch.zeros(32, 128, dtype=torch.float16, device=gpu)).shape == (0, 16)
 
 
 def _check_argmax(tokens, logits64, what):
