@@ -80,6 +80,21 @@ def test_attention_chunk_boundaries(gpu, model, q_len):
     check_against_oracle(w, 2, o, lse, f"edges q_len={q_len}")
 
 
+@pytest.mark.parametrize("hq,hkv,q_len", [(8, 8, 5), (40, 8, 5), (40, 8, 1), (64, 8, 5), (64, 8, 9), (32, 4, 1)],
+                         ids=["gqa1-q5", "gqa5-q5", "gqa5-q1", "gqa8-q5", "gqa8-q9", "32x4-q1"])
+def test_attention_gqa_ratios(gpu, hq, hkv, q_len):
+    """Head layouts beyond the two benchmark models: one q-head per kv head,
+    the Qwen3-14B (40/8) and Qwen3-32B (64/8) groups, and four kv heads.
+    With 8 q-heads per kv head a 9-row verify group is 72 rows, more than one
+    64-row MFMA group holds, so the planner splits it into 8 + 1 rows."""
+    model = dict(QWEN3_8B, num_attention_heads=hq, num_key_value_heads=hkv)
+    w = make_workload("target_verify", 4, device=gpu, num_layers=2, q_len=q_len, model=model)
+    o, lse, _ = run_attention(w, 1)
+    check_against_oracle(w, 1, o, lse, f"gqa {hq}/{hkv} q_len={q_len}")
+    del w
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("q_len", [12, 16], ids=["48rows", "64rows"])
 def test_attention_long_contexts_wide_groups(gpu, q_len):
     """48- and 64-row groups over log-uniform contexts up to 32k: segments cut

@@ -138,7 +138,9 @@ def test_rope_table_matches_oracle(gpu):
         assert (err <= bound).all(), f"{what} table: max excess {(err - bound).max():.3g}"
 
 
-@pytest.mark.parametrize("name,model", [("draft_decode", QWEN3_0_6B), ("target_verify", QWEN3_8B)])
+@pytest.mark.parametrize("name,model", [("draft_decode", QWEN3_0_6B), ("target_verify", QWEN3_8B),
+                                        ("target_verify", dict(QWEN3_8B, num_attention_heads=40))],
+                         ids=["0.6b", "8b", "40q-8kv"])
 def test_fused_prologue_matches_oracle(gpu, name, model):
     """QK-RMSNorm (gamma ~ U[0.5,1.5]) + RoPE (theta 1e6) + KV store for the new rows."""
     w = make_workload(name, 2, device=gpu)
