@@ -987,7 +987,10 @@ def measure_spec_loop(seed: int, steps: int, cpu_seconds: float) -> dict:
     attention over all of the model's layers (`steps` timed passes, the
     forward's own rows, lengths and caches).  Reports µs per layer call at
     the observed draft and target shapes, the CPU baseline at one sampled
-    shape of each, and the loop's own counters.
+    shape of each, and the loop's own counters.  Then runs the same loop
+    twice more with no sampling, its decode/verify layers once through the
+    native decoder stack and once from Python, and reports the decode
+    tokens per second of each (`throughput`).
     """
     import numpy as np
     import torch
@@ -1037,6 +1040,16 @@ def measure_spec_loop(seed: int, steps: int, cpu_seconds: float) -> dict:
     wall = time.perf_counter() - t0
     out = {"workload": "spec_loop_shapes", "loop": {k: v for k, v in res.items()},
            "bench_wall_s": wall}
+    thr = {}
+    for native in (True, False):
+        r = run(n_requests=64, prompt_lo=128, prompt_hi=1024, new_tokens=32, draft_batch=64, target_batch=16,
+                depth=4, seed=seed, device=dev, native=native)
+        thr["native_decoder_stack" if native else "python_layers"] = {
+            "decode_tokens_per_s": r["decode_tokens_per_s"], "wall_s": r["wall_s"], "prefill_s": r["prefill_s"],
+            "rounds": r["rounds"], "generated_tokens": r["generated_tokens"]}
+        torch.cuda.empty_cache()
+    out["throughput"] = dict(thr, config="64 requests x 32 generated tokens, prompts U[128, 1024], draft batch 64, "
+                                         "target batch 16, depth 4, no sampled checks")
     for role, xs in samples.items():
         if not xs:
             continue
@@ -1241,7 +1254,10 @@ def main():
         r2 = measure_spec_loop(args.seed, args.steps, args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
         print("# speculative loop shapes: " + "; ".join(
             f"{role} {r2[role]['us_per_layer_call_median']:.1f} us/layer-call over {r2[role]['samples']} forwards"
-            for role in ("draft", "target") if role in r2), file=sys.stderr, flush=True)
+            for role in ("draft", "target") if role in r2) + "; decode %.0f tokens/s (native decoder stack), %.0f "
+              "(layers from Python)" % (r2["throughput"]["native_decoder_stack"]["decode_tokens_per_s"],
+                                         r2["throughput"]["python_layers"]["decode_tokens_per_s"]),
+              file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     line = {
         "metric": "verify/decode attn µs per layer + HBM GB/s (% peak), Qwen3-8B B=16 q_len=5",

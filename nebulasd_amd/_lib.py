@@ -89,6 +89,13 @@ SIGNATURES = {
     "nsd_fused_add_rmsnorm_inplace": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]),
     "nsd_silu_and_mul_inplace": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "nsd_up_gate_silu_and_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "nsd_decoder_create": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_int,
+                                   POINTER(c_void_p)]),
+    "nsd_decoder_destroy": (c_int, [c_void_p]),
+    "nsd_decoder_forward": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                c_void_p, c_void_p, c_void_p, c_void_p, c_int64, _I32P, c_void_p, c_void_p, c_int64, c_float,
+                c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "nsd_lm_head_argmax": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "nsd_argmax_rows": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "nsd_probe_stream_read": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),

@@ -19,7 +19,10 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "_lib"
 LIB_PATH = LIB_DIR / "libnsd_attn.so"
-SOURCES = ["nsd_host.cpp", "nsd_prologue.hip", "nsd_attention.hip", "nsd_prefill.hip", "nsd_blocks.hip", "nsd_hostkv.hip", "nsd_layer.hip", "nsd_probe.hip"]
+SOURCES = ["nsd_host.cpp", "nsd_prologue.hip", "nsd_attention.hip", "nsd_prefill.hip", "nsd_blocks.hip", "nsd_hostkv.hip",
+           "nsd_layer.hip", "nsd_probe.hip", "nsd_decoder.hip"]
+# hipBLASLt, for the decoder executor's projection GEMMs (nsd_decoder.hip)
+LIBS = ["-lhipblaslt"]
 ARCH = "gfx950"
 
 
@@ -52,7 +55,7 @@ def compile_commands(obj_dir: Path) -> list[list[str]]:
 
 def link_command(obj_dir: Path, out: Path) -> list[str]:
     objs = [str(obj_dir / (Path(s).stem + ".o")) for s in SOURCES]
-    return [hipcc(), f"--offload-arch={ARCH}", "--hip-link", "-shared", "-fPIC", *objs, "-o", str(out)]
+    return [hipcc(), f"--offload-arch={ARCH}", "--hip-link", "-shared", "-fPIC", *objs, *LIBS, "-o", str(out)]
 
 
 def _run(cmds: list[list[str]], verbose: bool) -> None:

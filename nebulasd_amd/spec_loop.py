@@ -54,14 +54,22 @@ from .infer_state import build_infer_state, model_rope_cache
 from .kernels import (FUSED_UP_GATE_MAX_ROWS, flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention,
                       post_layer_forward, qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace,
                       silu_and_mul_inplace, store_kvcache, up_gate_silu_and_mul)
+from .decoder import MAX_ROWS as DECODER_MAX_ROWS
+from .decoder import DecoderStack
+from .phases import ENABLED as PHASE_RANGES
 from .phases import forward_phase_range
 from .speculative import compute_greedy_acceptance
 
 
 class RandomQwen3:
-    """A random-init Qwen3 decoder with a paged KV cache of its own."""
+    """A random-init Qwen3 decoder with a paged KV cache of its own.
 
-    def __init__(self, cfg: dict, seq_blocks: list, device, seed: int, std: float = 0.02):
+    ``native``: decode/verify forwards of up to 128 rows run their layers in
+    one call of the native decoder stack (``DecoderStack``), the same kernels
+    and GEMMs enqueued from C++; otherwise (and always for prompts, or with
+    the forward-phase ranges on) the layers run from Python as below."""
+
+    def __init__(self, cfg: dict, seq_blocks: list, device, seed: int, std: float = 0.02, native: bool = True):
         self.mc = mc = ModelConfig(cfg)
         self.dev = dev = torch.device(device)
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -99,6 +107,8 @@ class RandomQwen3:
         self.v_cache = torch.zeros(shape, dtype=torch.float16, device=dev)
         self.cos, self.sin = model_rope_cache(mc, width * 16 + 1, dev)
         self.check = None  # (layer, callback) of a sampled attention check
+        self.native = native
+        self.stack = None  # the native decoder stack, built on first use
 
     def _forward(self, st, token_ids: list, attention) -> list:
         """transformer_layer.py:83-201 for every layer, then model.py:292 and
@@ -161,6 +171,8 @@ class RandomQwen3:
         rising by one); returns the greedy next token of every row."""
         mc, dev = self.mc, self.dev
         st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
+        if self.native and len(tokens) <= DECODER_MAX_ROWS and not PHASE_RANGES:
+            return self._decode_native(st, seq_ids, seq_lens, tokens)
         hq = mc.num_q_heads
 
         def attention(li, lw, q_rows, k, v):
@@ -183,6 +195,26 @@ class RandomQwen3:
             return o
         return self._forward(st, tokens, attention)
 
+    def _decode_native(self, st, seq_ids: list, seq_lens: list, tokens: list) -> list:
+        """decode() with every layer in one call of the native decoder stack;
+        a sampled attention check receives its layer's q, o and LSE after
+        the forward (later layers write only their own cache slots)."""
+        mc, dev = self.mc, self.dev
+        if self.stack is None:
+            self.stack = DecoderStack(mc, self.layers)
+        x = self.embed[torch.tensor(tokens, device=dev)]
+        res = torch.zeros_like(x)
+        probe_layer = self.check[0] if self.check is not None else -1
+        probe = self.stack.forward(x, res, self.k_cache, self.v_cache, self.block_table, self.ec, st, self.cos,
+                                   self.sin, probe_layer)
+        if probe is not None:
+            q, o, lse = probe
+            self.check[1](self, probe_layer, q, o, lse, seq_ids, seq_lens)
+            self.check = None
+        x += res
+        with forward_phase_range("post_lm_head"):
+            return post_layer_forward(x, st, self.final_norm, self.lm_head, mc.rms_norm_eps).tolist()
+
 
 def _sync(dev: torch.device) -> None:
     if dev.type == "cuda":
@@ -192,7 +224,7 @@ def _sync(dev: torch.device) -> None:
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
         target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
         draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, share_weights=False, return_outputs=False,
-        log=None) -> dict:
+        log=None, native=True) -> dict:
     """The speculative loop over `n_requests` synthetic requests; returns a summary.
 
     With ``check_every`` > 0, every check_every-th forward calls
@@ -212,11 +244,11 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     prompts = [rng.integers(0, vocab, n).tolist() for n in plens]
     # room for the prompt, the output and one proposal beyond it
     blocks = [math.ceil((p + new_tokens + depth + 2) / 16) for p in plens]
-    target = RandomQwen3(target_cfg, blocks, dev, seed + 1)
+    target = RandomQwen3(target_cfg, blocks, dev, seed + 1, native=native)
     if share_weights:
-        draft = RandomQwen3(target_cfg, blocks, dev, seed + 1)
+        draft = RandomQwen3(target_cfg, blocks, dev, seed + 1, native=native)
     else:
-        draft = RandomQwen3(draft_cfg, blocks, dev, seed + 2)
+        draft = RandomQwen3(draft_cfg, blocks, dev, seed + 2, native=native)
     n_checks = 0
     t0 = time.perf_counter()
 
@@ -328,9 +360,12 @@ def main():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--share-weights", action="store_true",
                    help="draft = the target's model and weights (proposals accepted)")
+    p.add_argument("--python-layers", action="store_true",
+                   help="run decode/verify layers from Python instead of the native decoder stack")
     a = p.parse_args()
     res = run(a.requests, a.prompt_lo, a.prompt_hi, a.new_tokens, a.draft_batch, a.target_batch,
-              a.depth, a.seed, share_weights=a.share_weights, log=lambda m: print(m, flush=True))
+              a.depth, a.seed, share_weights=a.share_weights, log=lambda m: print(m, flush=True),
+              native=not a.python_layers)
     print(json.dumps(res), flush=True)
 
 

@@ -43,7 +43,7 @@ class ScriptedModel:
 
     mode = "exact"  # "exact": draft = target; "some": wrong a third of the time; "never"
 
-    def __init__(self, cfg, seq_blocks, device, seed):
+    def __init__(self, cfg, seq_blocks, device, seed, native=True):
         self.mc = ModelConfig(cfg)
         self.is_draft = self.mc.num_layers != QWEN3_8B["num_hidden_layers"]
         self.cache = {}
