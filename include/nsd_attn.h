@@ -154,7 +154,7 @@ int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_
  *   - the (group, kv head, 16-token block) stream is cut into n_workers
  *     contiguous ranges of near-equal cost (blocks plus a fixed charge per
  *     range piece), one per workgroup; a (group, kv head) segment cut
- *     across ranges gets fp32 partials (normalised O and log2-sum-exp),
+ *     across ranges gets partials (normalised O in fp16, log2-sum-exp in fp32),
  *     merged in slot order by a second launch of the same call.
  * nsd_attn_plan_bound gives the plan size in int32 words for plans that fit
  * n_workers workers.  A plan may use more workers than asked (a worker

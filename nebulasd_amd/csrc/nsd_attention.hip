@@ -38,7 +38,9 @@
 // blocks of a step belong to one piece; a piece with an odd block count ends
 // with a one-block step (its second half masked, both halves read from the
 // one slot).  Segments cut across
-// workers write fp32 partials (normalised O, log2-sum-exp), and a second,
+// workers write partials (normalised O in fp16, log2-sum-exp in fp32: the
+// merged result stays within one more fp16 rounding of the fp32 merge, and
+// the partial stores, a few MB per call, cost half the time), and a second,
 // small launch merges each such segment's partials in slot order (the
 // reference's phase 2): the attention kernel then ends as soon as its
 // workgroups have stored their last results.
@@ -102,7 +104,7 @@ struct AttnArgs {
   int64_t bt_stride;
   const int32_t* workers;  // plan: worker table
   const int32_t* pieces;   // plan: piece records
-  float* part_o;           // [slots, rows_max, D]
+  f16* part_o;             // [slots, rows_max, D]  normalised O
   float* part_lse;         // [slots, rows_max]  (log2 domain)
   const int32_t* combines; // plan: combine records of the segments cut across workers
   int32_t* status;
@@ -181,9 +183,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a, int row_groups
   const int h = c[kCombHead], first = c[kCombFirst], n_slots = c[kCombSlots];
   if (n >= c[kCombQLen] * a.gqa) return;
   const int d8 = threadIdx.x & 15;
-  const float* po = a.part_o + ((int64_t)first * a.rows_max + n) * D + 8 * d8;
+  const f16* po = a.part_o + ((int64_t)first * a.rows_max + n) * D + 8 * d8;
   const float* pl = a.part_lse + (int64_t)first * a.rows_max + n;
-  const int64_t sstride = (int64_t)a.rows_max * D;  // floats between slots
+  const int64_t sstride = (int64_t)a.rows_max * D;  // elements between slots
   float M = -INFINITY, W = 0.f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < n_slots; s0 += 8) {
@@ -193,8 +195,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a, int row_groups
     for (int u = 0; u < 8; ++u) {
       const int sidx = s0 + u < n_slots ? s0 + u : s0;
       ls[u] = s0 + u < n_slots ? pl[(int64_t)sidx * a.rows_max] : -INFINITY;
-      v0[u] = *reinterpret_cast<const f32x4*>(po + sidx * sstride);
-      v1[u] = *reinterpret_cast<const f32x4*>(po + sidx * sstride + 4);
+      const f16x8 h = *reinterpret_cast<const f16x8*>(po + sidx * sstride);
+      v0[u] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+      v1[u] = f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
     }
     float mb = M;
 #pragma unroll
@@ -365,12 +368,55 @@ void paged_attn_kernel(AttnArgs a) {
       }
   };
   if (n_pc > 0) start_piece(0);
+  // End of piece p: this wave's 16 rows of the output, or of the segment's
+  // partial.
+  auto store_piece = [&](int p) __attribute__((always_inline)) {
+    if (!computes) return;
+    const float lt = rows_sum(l);
+    const int n = 16 * wave + lr;
+    if (n < rec(p, kPieceQLen) * a.gqa) {
+      const int slot = rec(p, kPieceSlot);
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      const float lse2 = lt > 0.f ? m + __log2f(lt) : -INFINITY;
+      const int qi = n / a.gqa, gh = n - qi * a.gqa;
+      const int64_t orow = (int64_t)(rec(p, kPieceRowStart) + qi) * a.hq + rec(p, kPieceHead) * a.gqa + gh;
+      if (slot < 0) {
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+          const f32x4 ov = acc[mt] * inv;
+          f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
+          *reinterpret_cast<f16x4*>(a.o + orow * D + 16 * mt + 4 * lg) = hv;
+        }
+        if (lg == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
+      } else {
+        f16* po = a.part_o + ((int64_t)slot * a.rows_max + n) * D + 4 * lg;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+          const f32x4 ov = acc[mt] * inv;
+          f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
+          *reinterpret_cast<f16x4*>(po + 16 * mt) = hv;
+        }
+        if (lg == 0) a.part_lse[(int64_t)slot * a.rows_max + n] = lse2;
+      }
+    }
+  };
 
+  int done = -1;  // a finished piece whose rows are not stored yet
   for (int i = 0; i < n_items;) {
     // two blocks of the piece, or its last one
     const int step = ck + 2 <= c_items ? 2 : 1;
     wait_ring(issued - i - step);  // this step's blocks landed (this wave's part) ...
     barrier();                     // ... and every wave's; the previous step's slots are free
+    // The piece that ended with the previous step is stored here, ahead of
+    // this step's loads: the stores then complete in the shadow of those
+    // loads instead of delaying the wait for them (a wave's vmcnt retires
+    // its memory operations in order, stores included).  The accumulators
+    // are reset for the next piece after that.
+    if (done >= 0) {
+      store_piece(done);
+      done = -1;
+      start_piece(cp);
+    }
     while (issued < n_items && issued < i + kRing) issue();
     const lds_char* sa = ring + cslot * kSlot;
     const lds_char* sb = step == 2 ? ring + (cslot + 1 == kRing ? 0 : cslot + 1) * kSlot : sa;
@@ -446,44 +492,16 @@ void paged_attn_kernel(AttnArgs a) {
     ck += step;
     cslot += step;
     if (cslot >= kRing) cslot -= kRing;
-    if (ck == c_items) {
-      // end of the piece: this wave's 16 rows of the output, or of the
-      // segment's partial
-      if (computes) {
-        const float lt = rows_sum(l);
-        const int n = 16 * wave + lr;
-        if (n < rec(cp, kPieceQLen) * a.gqa) {
-          const int slot = rec(cp, kPieceSlot);
-          const float inv = lt > 0.f ? 1.f / lt : 0.f;
-          const float lse2 = lt > 0.f ? m + __log2f(lt) : -INFINITY;
-          const int qi = n / a.gqa, gh = n - qi * a.gqa;
-          const int64_t orow = (int64_t)(rec(cp, kPieceRowStart) + qi) * a.hq +
-                               rec(cp, kPieceHead) * a.gqa + gh;
-          if (slot < 0) {
-#pragma unroll
-            for (int mt = 0; mt < 8; ++mt) {
-              const f32x4 ov = acc[mt] * inv;
-              f16x4 hv = {(f16)ov[0], (f16)ov[1], (f16)ov[2], (f16)ov[3]};
-              *reinterpret_cast<f16x4*>(a.o + orow * D + 16 * mt + 4 * lg) = hv;
-            }
-            if (lg == 0 && a.lse != nullptr) a.lse[orow] = lse2 * kLn2;
-          } else {
-            float* po = a.part_o + ((int64_t)slot * a.rows_max + n) * D + 4 * lg;
-#pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
-              *reinterpret_cast<f32x4*>(po + 16 * mt) = acc[mt] * inv;
-            if (lg == 0) a.part_lse[(int64_t)slot * a.rows_max + n] = lse2;
-          }
-        }
-      }
+    if (ck == c_items) {  // end of the piece: stored after the next barrier
+      done = cp;
       ck = 0;
       if (++cp < n_pc) {
         c_items = items_of(cp);
         c_blk0 = rec(cp, kPieceBlkBegin);
-        start_piece(cp);
       }
     }
   }
+  if (done >= 0) store_piece(done);
 
 }
 
@@ -539,11 +557,10 @@ static __device__ __align__(256) char scratch[NSD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
-// Bytes of the fp32 partials a plan needs: normalised O and log2-sum-exp
-// per partial slot, rounded up to 256 bytes.
+// Bytes of the partials a plan needs: normalised O (fp16) and log2-sum-exp
+// (fp32) per partial slot and row, rounded up to 256 bytes.
 int64_t plan_partial_bytes(const int32_t* plan_host) {
-  return ((int64_t)plan_host[kPlanSlots] * plan_host[kPlanRowsMax] * (int64_t)(D + 1) * 4 + 255) /
-         256 * 256;
+  return ((int64_t)plan_host[kPlanSlots] * plan_host[kPlanRowsMax] * (int64_t)(D * 2 + 4) + 255) / 256 * 256;
 }
 
 // Shared body of the two attention entry points: `part` holds the partials
@@ -647,8 +664,8 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
   args.bt_stride = bt_stride;
   args.workers = plan_dev + plan_host[kPlanOffWorkers];
   args.pieces = plan_dev + plan_host[kPlanOffPieces];
-  args.part_o = static_cast<float*>(part);
-  args.part_lse = static_cast<float*>(part) + n_slots * rows_max * D;
+  args.part_o = static_cast<f16*>(part);
+  args.part_lse = reinterpret_cast<float*>(static_cast<f16*>(part) + n_slots * rows_max * D);
   args.combines = plan_dev + plan_host[kPlanOffCombines];
   args.status = status;
   args.num_blocks = num_blocks;

@@ -284,8 +284,8 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   std::copy(combines.begin(), combines.end(), h + off_combines);
 
   *plan_words = words;
-  // partial O and log-sum-exp per slot
-  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(kHeadDim + 1) * 4 + 255) / 256 * 256;
+  // partial O (fp16) and log-sum-exp (fp32) per slot and row
+  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(kHeadDim * 2 + 4) + 255) / 256 * 256;
   *workspace_bytes = n_combines > 0 ? part_bytes : 0;
   return NSD_OK;
 }

@@ -160,7 +160,7 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
                                block_size, bt_rows, bt_stride,
                                num_workers(rows_max, device.index), max_group_rows)
     dev = torch.from_numpy(words).to(device, non_blocking=False)
-    # the split segments' fp32 partials; every launch writes each slot before
+    # the split segments' partials; every launch writes each slot before
     # the merge reads it, so the buffer needs no initialisation
     workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=device)
     return AttnPlan(words, dev, workspace, ws, num_q_heads, num_kv_heads)

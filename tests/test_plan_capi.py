@@ -214,8 +214,8 @@ def test_plan_invariants_random(lib, seed):
     for hq, hkv in ((32, 8), (16, 8), (8, 8)):
         p, ws = _plan(seq_ids, seq_lens, hq, hkv, workers, bt_rows=100)
         check_plan_invariants(p, seq_ids, seq_lens, hkv, hq // hkv)
-        # partials: fp32 O + lse per slot row
-        part = -(-p["slots"] * p["rows_max"] * 129 * 4 // 256) * 256
+        # partials: fp16 O (128 x 2 bytes) + fp32 lse per slot row
+        part = -(-p["slots"] * p["rows_max"] * (128 * 2 + 4) // 256) * 256
         assert ws == (part if len(p["combines"]) else 0)
 
 
@@ -368,7 +368,7 @@ def test_noalloc_rejects_plans_larger_than_its_scratch(lib):
     slens = [32000 + i + 1 for _ in range(32) for i in range(16)]
     words, _ = plan_words(sids, slens, 32, 8, 128, 16, 32, 2100, 2048)
     slots, rows_max = int(words[_lib.PLAN_SLOTS]), int(words[_lib.PLAN_ROWS_MAX])
-    assert slots * rows_max * 129 * 4 > (16 << 20), "the plan should not fit the scratch"
+    assert slots * rows_max * (128 * 2 + 4) > (16 << 20), "the plan should not fit the scratch"
     rc = lib.nsd_paged_attention_noalloc(
         None, None, None, None, None, 24576, 36, 0, 32, 8, 128, 16, None, 32, 2100,
         words.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), None, 0.088, None, None)
