@@ -387,6 +387,55 @@ int nsd_up_gate_silu_and_mul(const void* x, const void* up_gate, void* y, int64_
                              int64_t hidden, int64_t inter, void* stream);
 
 /*
+ * Split-k projection GEMM for decode/verify batches: the layer's q/k/v, O
+ * and down projections (swiftLLM/swiftllm/worker/layers/transformer_layer.py:
+ * 107-109, 187, 201, each `linear(x, W)` = F.linear, kernels/linear.py:3-12)
+ * for n_rows <= 128.  partials [splits][n_rows][n_out] fp32 receives, per
+ * split s, sum over k in split s's range of x[r][k] * W[j][k] (x [n_rows,
+ * n_in], W [n_out, n_in] fp16 row-major); the projection is the sum of the
+ * splits in split order rounded once to fp16, which nsd_sum_partials,
+ * nsd_fused_add_rmsnorm_partials and nsd_qk_norm_rope_store_partials compute
+ * where they read it.  nsd_linear_splits gives the split count (1..8) the
+ * current device uses for a shape, to size `partials`.  n_out a multiple of
+ * 16, n_in a multiple of 128, pointers 16-byte aligned.
+ */
+int nsd_linear_splits(int64_t n_rows, int64_t n_out, int64_t n_in, int* splits);
+int nsd_linear_partials(const void* x, const void* w, float* partials, int64_t n_rows, int64_t n_out,
+                        int64_t n_in, void* stream);
+
+/*
+ * nsd_sum_partials: y [n_rows, n_out] fp16 = fp16(sum over s < splits of
+ * partials[s]) (split order): the projection nsd_linear_partials computed.
+ */
+int nsd_sum_partials(const float* partials, int splits, void* y, int64_t n_rows, int64_t n_out,
+                     void* stream);
+
+/*
+ * nsd_fused_add_rmsnorm_partials: nsd_fused_add_rmsnorm_inplace whose x is a
+ * projection given as split partials (the linear before fused_add_rmsnorm_inplace
+ * in transformer_layer.py:187-192 and, across layers, :201 then :98-103):
+ * residual += fp16(sum of the splits), out = the normalised residual.
+ */
+int nsd_fused_add_rmsnorm_partials(const float* partials, int splits, void* out, void* residual,
+                                   const void* weight, int64_t n_rows, int64_t hidden, float eps,
+                                   void* stream);
+
+/*
+ * nsd_qk_norm_rope_store_partials: nsd_qk_norm_rope_store_strided over the
+ * fused q/k/v projection given as split partials [splits][n_rows][(Hq +
+ * 2*Hkv) * d] (transformer_layer.py:107-145): q normalised and rotated into
+ * q_out [n_rows, Hq, d], K and V written to the cache slots of the rows.
+ */
+int nsd_qk_norm_rope_store_partials(const float* partials, int splits, void* q_out, const void* q_norm_w,
+                                    const void* k_norm_w, float eps, const void* cos_cache,
+                                    const void* sin_cache, int64_t n_positions, void* k_cache,
+                                    void* v_cache, const int32_t* block_table, int64_t bt_rows,
+                                    int64_t bt_stride, const int32_t* seq_ids, const int32_t* seq_lens,
+                                    int64_t n_rows, int64_t num_blocks, int num_layers, int layer,
+                                    int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                    int32_t* status, void* stream);
+
+/*
  * nsd_lm_head_argmax: the post-layer's logits and argmax
  * (swiftLLM/swiftllm/worker/layers/post_layer.py:70-71,
  * `argmax(linear(last_input, lm_head), dim=1)`) without the logits tensor:

@@ -16,14 +16,15 @@
  *   h = fp16(up) * fp16(silu(fp16(gate))) of o . W_up_gate^T     (:199-200)
  *   x = h . W_down^T                                             (:201)
  *
- * on this library's kernels (nsd_attn.h) and, for the q/k/v, O and down
- * projections, hipBLASLt GEMMs (fp16 in and out, fp32 sums), all enqueued on
- * the caller's stream from C++: the host cost of a layer is a dozen launches
- * instead of a dozen Python calls.  The embedding lookup before the stack
- * and the final residual add and post-layer after it stay with the caller.
+ * on this library's kernels (nsd_attn.h), the q/k/v, O and down projections
+ * included (nsd_linear_partials, whose split partials the next kernel sums
+ * where it reads the projection), all enqueued on the caller's stream from
+ * C++: the host cost of a layer is ten launches instead of a dozen Python
+ * calls.  The embedding lookup before the stack and the final residual add
+ * and post-layer after it stay with the caller.
  *
  * nsd_decoder_create allocates the executor's device buffers (activations
- * for up to max_rows rows and a 32 MiB GEMM workspace) and keeps the layer
+ * and projection partials for up to max_rows rows) and keeps the layer
  * weight pointers, which must stay valid until nsd_decoder_destroy.
  * nsd_decoder_forward allocates nothing and never synchronises the host; a
  * decoder serves one stream at a time (its activation buffers are shared
@@ -54,7 +55,7 @@ typedef struct nsd_decoder_layer {
   const void* k_norm;     /* [d] k RMSNorm weight, or NULL */
 } nsd_decoder_layer;
 
-/* hidden a multiple of 128 (<= 8192), inter a multiple of 16, head_dim 128,
+/* hidden a multiple of 128 (<= 8192), inter a multiple of 128, head_dim 128,
  * num_q_heads a multiple of num_kv_heads, 1 <= max_rows <= 128. */
 int nsd_decoder_create(int num_layers, int hidden, int inter, int num_q_heads, int num_kv_heads,
                        int head_dim, float rms_eps, const nsd_decoder_layer* layers, int max_rows,

@@ -89,6 +89,15 @@ SIGNATURES = {
     "nsd_fused_add_rmsnorm_inplace": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]),
     "nsd_silu_and_mul_inplace": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "nsd_up_gate_silu_and_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "nsd_linear_splits": (c_int, [c_int64, c_int64, c_int64, POINTER(c_int)]),
+    "nsd_linear_partials": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "nsd_sum_partials": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p]),
+    "nsd_fused_add_rmsnorm_partials": (
+        c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]),
+    "nsd_qk_norm_rope_store_partials": (
+        c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_void_p,
+                c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int,
+                c_int, c_int, c_int, c_void_p, c_void_p]),
     "nsd_decoder_create": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_int,
                                    POINTER(c_void_p)]),
     "nsd_decoder_destroy": (c_int, [c_void_p]),

@@ -20,9 +20,8 @@ CSRC = PKG / "csrc"
 LIB_DIR = PKG / "_lib"
 LIB_PATH = LIB_DIR / "libnsd_attn.so"
 SOURCES = ["nsd_host.cpp", "nsd_prologue.hip", "nsd_attention.hip", "nsd_prefill.hip", "nsd_blocks.hip", "nsd_hostkv.hip",
-           "nsd_layer.hip", "nsd_probe.hip", "nsd_decoder.hip"]
-# hipBLASLt, for the decoder executor's projection GEMMs (nsd_decoder.hip)
-LIBS = ["-lhipblaslt"]
+           "nsd_layer.hip", "nsd_probe.hip", "nsd_decoder.hip", "nsd_gemm.hip"]
+LIBS: list[str] = []  # the HIP runtime only
 ARCH = "gfx950"
 
 

@@ -34,10 +34,14 @@ typedef __attribute__((address_space(1))) u32x4 gbl_u32x4;
 __device__ inline f16x8 as_h8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 __device__ inline u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
+// With `part` set, x is the projection whose fp32 split partials part holds
+// ([splits][rows][hidden]): summed in split order and rounded to fp16 (the
+// GEMM's output rounding) in place of reading x; the normalised row is
+// written to x either way.
 template <int VPT>
 __global__ void __launch_bounds__(kNormThreads)
 fused_add_rmsnorm_kernel(f16* __restrict__ x, f16* __restrict__ res, const f16* __restrict__ w, int nvec,
-                         int hidden, float eps) {
+                         int hidden, float eps, const float* __restrict__ part, int splits, int64_t split_stride) {
   __shared__ float s_part[kNormThreads / kWave];
   const int64_t row = blockIdx.x;
   u32x4* xr = reinterpret_cast<u32x4*>(x + row * hidden);
@@ -49,7 +53,19 @@ fused_add_rmsnorm_kernel(f16* __restrict__ x, f16* __restrict__ res, const f16* 
   for (int j = 0; j < VPT; ++j) {
     const int i = threadIdx.x + j * kNormThreads;
     if (i < nvec) {
-      const f16x8 a = as_h8(xr[i]), b = as_h8(rr[i]);
+      f16x8 a;
+      if (part != nullptr) {
+        const float* p = part + row * hidden + 8 * i;
+        f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+        for (int q = 1; q < splits; ++q) {
+          lo += *reinterpret_cast<const f32x4*>(p + q * split_stride);
+          hi += *reinterpret_cast<const f32x4*>(p + q * split_stride + 4);
+        }
+        a = f16x8{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3], (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
+      } else {
+        a = as_h8(xr[i]);
+      }
+      const f16x8 b = as_h8(rr[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         s[j][e] = (f16)((float)a[e] + (float)b[e]);  // one fp16 rounding, as an fp16 add
@@ -552,15 +568,15 @@ void launch_ug_rows(std::integer_sequence<int, N...>, int nrt, int to, const f16
 
 using namespace nsd;
 
-extern "C" int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void* weight, int64_t n_rows,
-                                             int64_t hidden, float eps, void* stream) {
+static int fused_add_rmsnorm(void* x, void* residual, const void* weight, int64_t n_rows, int64_t hidden, float eps,
+                             const float* part, int splits, void* stream) {
   if (n_rows < 0 || hidden <= 0) return fail(NSD_ERR_INVALID, "fused_add_rmsnorm: bad shape");
   if (n_rows == 0) return NSD_OK;
   if (!x || !residual || !weight) return fail(NSD_ERR_INVALID, "fused_add_rmsnorm: null pointer");
   if (hidden % 8 || hidden > 8 * kNormThreads * kMaxNormVecs)
     return fail(NSD_ERR_UNSUPPORTED, "fused_add_rmsnorm: hidden=%lld (need a multiple of 8, <= %d)",
                 (long long)hidden, 8 * kNormThreads * kMaxNormVecs);
-  if (!aligned16(x) || !aligned16(residual) || !aligned16(weight))
+  if (!aligned16(x) || !aligned16(residual) || !aligned16(weight) || (part && !aligned16(part)))
     return fail(NSD_ERR_UNSUPPORTED, "fused_add_rmsnorm: pointers must be 16-byte aligned");
   if (n_rows > INT32_MAX) return fail(NSD_ERR_UNSUPPORTED, "fused_add_rmsnorm: too many rows");
   const int nvec = (int)(hidden / 8);
@@ -568,7 +584,7 @@ extern "C" int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3((unsigned)n_rows), dim3(kNormThreads), 0, as_stream(stream),
                        static_cast<f16*>(x), static_cast<f16*>(residual), static_cast<const f16*>(weight), nvec,
-                       (int)hidden, eps);
+                       (int)hidden, eps, part, splits, n_rows * hidden);
   };
   switch (vpt) {
     case 1: go(fused_add_rmsnorm_kernel<1>); break;
@@ -577,6 +593,19 @@ extern "C" int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void
     default: go(fused_add_rmsnorm_kernel<4>); break;
   }
   return launch_status("fused_add_rmsnorm");
+}
+
+extern "C" int nsd_fused_add_rmsnorm_inplace(void* x, void* residual, const void* weight, int64_t n_rows,
+                                             int64_t hidden, float eps, void* stream) {
+  return fused_add_rmsnorm(x, residual, weight, n_rows, hidden, eps, nullptr, 1, stream);
+}
+
+extern "C" int nsd_fused_add_rmsnorm_partials(const float* partials, int splits, void* out, void* residual,
+                                              const void* weight, int64_t n_rows, int64_t hidden, float eps,
+                                              void* stream) {
+  if (partials == nullptr || splits < 1 || splits > 8)
+    return fail(NSD_ERR_INVALID, "fused_add_rmsnorm_partials: %d splits (1..8) of partials", splits);
+  return fused_add_rmsnorm(out, residual, weight, n_rows, hidden, eps, partials, splits, stream);
 }
 
 extern "C" int nsd_silu_and_mul_inplace(void* x, int64_t n_tokens, int64_t inter_dim, void* stream) {

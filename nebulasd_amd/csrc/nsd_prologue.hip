@@ -130,7 +130,11 @@ __global__ __launch_bounds__(256) void rope_kernel(f16* __restrict__ q, f16* __r
 // fused q/k/v projection); k heads also write the rotated row to the cache
 // slot; v heads copy to it.  Rows of q, k and v are q_stride, k_stride and
 // v_stride elements apart.  Order and math of transformer_layer.py:114-145
-// in one launch.
+// in one launch.  With `part` set, the fused q/k/v projection is given as
+// fp32 split partials [splits][rows][q_stride] (q_stride = (hq + 2 hkv) D):
+// each element is summed in split order and rounded to fp16 (the GEMM's
+// output rounding) where it would be read, and k is written to the cache
+// only.
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
     const f16* q, int64_t q_stride, f16* q_out, f16* k, int64_t k_stride, const f16* __restrict__ v,
     int64_t v_stride,
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
     f16* __restrict__ kc, f16* __restrict__ vc, const int32_t* __restrict__ bt, int64_t bt_rows,
     int64_t bt_stride, const int32_t* __restrict__ seq_ids, const int32_t* __restrict__ seq_lens,
     int64_t n_rows, int64_t num_blocks, int num_layers, int layer, int hq, int hkv,
-    int32_t* status) {
+    int32_t* status, const float* __restrict__ part, int splits) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int heads = hq + 2 * hkv;
@@ -147,6 +151,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   const int64_t r = wid / heads;
   const int hd = (int)(wid % heads);
   const int64_t pos = (int64_t)seq_lens[r] - 1;
+  // element c of head hd of this row from the partials, as the GEMM's fp16 output
+  const int64_t split_stride = n_rows * q_stride;
+  auto from_part = [&](int c) {
+    const float* p = part + r * q_stride + (int64_t)hd * D + c;
+    float acc = p[0];
+    for (int q2 = 1; q2 < splits; ++q2) acc += p[q2 * split_stride];
+    return (f16)acc;
+  };
 
   int64_t slot = -1;  // element offset of (block, layer, head 0, pos % BS, 0)
   if (hd >= hq) {
@@ -165,9 +177,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   if (hd >= hq + hkv) {  // v head: bit-exact copy of 256 bytes
     const int h = hd - hq - hkv;
     if (slot >= 0) {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(v + r * v_stride + (int64_t)h * D);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(vc + slot + (int64_t)h * BS * D);
-      dst[lane] = src[lane];
+      if (part != nullptr) {
+        f16* dst = vc + slot + (int64_t)h * BS * D;
+        dst[lane] = from_part(lane);
+        dst[lane + 64] = from_part(lane + 64);
+      } else {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(v + r * v_stride + (int64_t)h * D);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(vc + slot + (int64_t)h * BS * D);
+        dst[lane] = src[lane];
+      }
     }
     return;
   }
@@ -177,10 +195,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   }
   const bool isk = hd >= hq;
   const int h = isk ? hd - hq : hd;
-  const f16* xin = isk ? k + r * k_stride + (int64_t)h * D : q + r * q_stride + (int64_t)h * D;
-  f16* x = isk ? k + r * k_stride + (int64_t)h * D : q_out + (r * hq + h) * D;
+  f16* x = isk ? (part != nullptr ? nullptr : k + r * k_stride + (int64_t)h * D) : q_out + (r * hq + h) * D;
   const f16* w = isk ? kw : qw;
-  float x0 = (float)xin[lane], x1 = (float)xin[lane + 64];
+  float x0, x1;
+  if (part != nullptr) {
+    x0 = (float)from_part(lane);
+    x1 = (float)from_part(lane + 64);
+  } else {
+    const f16* xin = isk ? k + r * k_stride + (int64_t)h * D : q + r * q_stride + (int64_t)h * D;
+    x0 = (float)xin[lane];
+    x1 = (float)xin[lane + 64];
+  }
   if (w != nullptr) {
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float rstd = 1.f / sqrtf(ss / (float)D + eps);
@@ -190,8 +215,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
   const float c = (float)cos_c[pos * (D / 2) + lane], s = (float)sin_c[pos * (D / 2) + lane];
   const f16 y0 = (f16)(x0 * c - x1 * s);
   const f16 y1 = (f16)(x0 * s + x1 * c);
-  x[lane] = y0;
-  x[lane + 64] = y1;
+  if (x != nullptr) {
+    x[lane] = y0;
+    x[lane + 64] = y1;
+  }
   if (isk && slot >= 0) {
     f16* dst = kc + slot + (int64_t)h * BS * D;
     dst[lane] = y0;
@@ -304,15 +331,15 @@ static int qk_norm_rope_store_impl(const void* q, int64_t q_stride, void* q_out,
                                    int64_t bt_stride, const int32_t* seq_ids, const int32_t* seq_lens,
                                    int64_t n_rows, int64_t num_blocks, int num_layers, int layer,
                                    int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                   int32_t* status, void* stream) {
+                                   int32_t* status, void* stream, const float* part = nullptr, int splits = 1) {
   int rc = check_cache_shape(num_layers, layer, num_kv_heads, head_dim, block_size, num_blocks,
                              "qk_norm_rope_store");
   if (rc) return rc;
   if (num_q_heads <= 0 || n_rows < 0 || n_positions <= 0 || bt_rows <= 0 || bt_stride <= 0)
     return fail(NSD_ERR_INVALID, "qk_norm_rope_store: bad sizes");
   if (n_rows == 0) return NSD_OK;
-  if (!q || !q_out || !k || !v || !cos_cache || !sin_cache || !k_cache || !v_cache || !block_table ||
-      !seq_ids || !seq_lens)
+  if ((part == nullptr && (!q || !k || !v)) || !q_out || !cos_cache || !sin_cache || !k_cache || !v_cache ||
+      !block_table || !seq_ids || !seq_lens)
     return fail(NSD_ERR_INVALID, "qk_norm_rope_store: null pointer");
   if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
     return fail(NSD_ERR_INVALID, "qk_norm_rope_store: pass both norm weights or neither");
@@ -327,7 +354,7 @@ static int qk_norm_rope_store_impl(const void* q, int64_t q_stride, void* q_out,
                      static_cast<const f16*>(cos_cache), static_cast<const f16*>(sin_cache), n_positions,
                      static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), block_table, bt_rows, bt_stride,
                      seq_ids, seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads, num_kv_heads,
-                     status);
+                     status, part, splits);
   return launch_status("qk_norm_rope_store");
 }
 
@@ -361,4 +388,21 @@ extern "C" int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_strid
                                  cos_cache, sin_cache, n_positions, k_cache, v_cache, block_table, bt_rows,
                                  bt_stride, seq_ids, seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads,
                                  num_kv_heads, head_dim, block_size, status, stream);
+}
+
+extern "C" int nsd_qk_norm_rope_store_partials(const float* partials, int splits, void* q_out, const void* q_norm_w,
+                                               const void* k_norm_w, float eps, const void* cos_cache,
+                                               const void* sin_cache, int64_t n_positions, void* k_cache,
+                                               void* v_cache, const int32_t* block_table, int64_t bt_rows,
+                                               int64_t bt_stride, const int32_t* seq_ids, const int32_t* seq_lens,
+                                               int64_t n_rows, int64_t num_blocks, int num_layers, int layer,
+                                               int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                               int32_t* status, void* stream) {
+  if (partials == nullptr || splits < 1 || splits > 8)
+    return fail(NSD_ERR_INVALID, "qk_norm_rope_store_partials: %d splits (1..8) of partials", splits);
+  const int64_t row_w = (int64_t)(num_q_heads + 2 * num_kv_heads) * head_dim;
+  return qk_norm_rope_store_impl(nullptr, row_w, q_out, nullptr, row_w, nullptr, row_w, q_norm_w, k_norm_w, eps,
+                                 cos_cache, sin_cache, n_positions, k_cache, v_cache, block_table, bt_rows,
+                                 bt_stride, seq_ids, seq_lens, n_rows, num_blocks, num_layers, layer, num_q_heads,
+                                 num_kv_heads, head_dim, block_size, status, stream, partials, splits);
 }

@@ -80,3 +80,42 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
                   k.stride(0), v.data_ptr(), v.stride(0), *tail)
     if status is not None:
         status.check("qk_norm_rope_store")
+
+
+def qk_norm_rope_store_partials(partials: torch.Tensor, q_out: torch.Tensor, k_cache: torch.Tensor,
+                                v_cache: torch.Tensor, block_table: torch.Tensor, q_norm: torch.Tensor | None,
+                                k_norm: torch.Tensor | None, model_config, engine_config, infer_state,
+                                cur_layer: int, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                                validate: bool = False) -> None:
+    """The prologue over the fused q/k/v projection of the decode/verify rows
+    given as split partials [splits, rows, (Hq + 2*Hkv) * d] (``linear_partials``):
+    q normalised and rotated into ``q_out`` [rows, Hq, d], K and V stored into
+    the cache slots of the rows (transformer_layer.py:107-145)."""
+    require_cuda(partials, q_out, k_cache, v_cache, block_table, cos_cache, sin_cache, q_norm, k_norm)
+    require(partials, torch.float32, "partials")
+    for t, n in ((q_out, "q_out"), (k_cache, "k_cache"), (v_cache, "v_cache"), (cos_cache, "cos_cache"),
+                 (sin_cache, "sin_cache")):
+        require(t, torch.float16, n)
+    check_block_table(block_table, engine_config)
+    if (q_norm is None) != (k_norm is None):
+        raise ValueError("pass both q_norm and k_norm, or neither")
+    n_blocks, n_layers, hkv, bs, d = cache_dims(k_cache)
+    rows, hq = infer_state.num_decoding_seqs, model_config.num_q_heads
+    if partials.dim() != 3 or tuple(partials.shape[1:]) != (rows, (hq + 2 * hkv) * d):
+        raise ValueError(f"partials must be [splits, {rows}, {(hq + 2 * hkv) * d}]")
+    if tuple(q_out.shape) != (rows, hq, d):
+        raise ValueError(f"q_out must be [{rows}, {hq}, {d}]")
+    if rows == 0:
+        return
+    if getattr(infer_state, "ignore_kvcache", False):
+        raise ValueError("infer_state.ignore_kvcache is set but the forward has decode rows")
+    npf = infer_state.num_prefill_seqs
+    status = StatusWord(q_out.device) if validate else None
+    _lib.call("nsd_qk_norm_rope_store_partials", partials.data_ptr(), partials.shape[0], q_out.data_ptr(),
+              ptr(q_norm), ptr(k_norm), float(model_config.rms_norm_eps), cos_cache.data_ptr(), sin_cache.data_ptr(),
+              cos_cache.shape[0], k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+              block_table.shape[0], block_table.shape[1], infer_state.seq_ids[npf:].data_ptr(),
+              infer_state.decoding_seq_lens.data_ptr(), rows, n_blocks, n_layers, int(cur_layer), hq, hkv, d, bs,
+              ptr(status.t) if status else None, stream_of(q_out))
+    if status is not None:
+        status.check("qk_norm_rope_store_partials")
