@@ -665,6 +665,62 @@ def measure_layer_step(seed: int, reps: int = 20):
                     "eager passes of four layers with distinct weights"}
 
 
+def measure_native_layers(seed: int, reps: int = 20) -> dict:
+    """The native decoder stack (nsd_decoder_forward: every layer enqueued
+    from C++ on this build's kernels, split-k projections included) over
+    four layers with distinct weights, graph-replayed: µs per layer at the
+    target-verify batch (Qwen3-8B, 16 requests x 5 rows, contexts
+    U[256, 4096]) and the draft batch (Qwen3-0.6B, 64 rows, contexts
+    U[512, 2048]); the weights of four layers (1.5 GB for Qwen3-8B) exceed
+    the 256 MB MALL, so each layer reads its weights from HBM."""
+    import numpy as np
+    import torch
+
+    from nebulasd_amd.config import EngineConfig, ModelConfig
+    from nebulasd_amd.decoder import DecoderStack
+    from nebulasd_amd.infer_state import build_infer_state, rope_cache
+    from nebulasd_amd.workload import make_workload
+
+    dev = torch.device("cuda:0")
+    out = {}
+    n_layers = 4
+    for name, workload in (("target_verify", "target_verify"), ("draft_decode", "draft_decode")):
+        w = make_workload(workload, seed, device=dev, num_layers=n_layers)
+        cfg = dict(w.spec.model, num_hidden_layers=n_layers)
+        mc = ModelConfig(cfg)
+        ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
+        cos, sin = rope_cache(128, mc.rope_theta, max(w.seq_lens) + 1, dev)
+        st = build_infer_state(w.seq_ids, w.seq_lens, [], mc, cos, sin, dev)
+        H, I, hq, hkv, d = mc.hidden_size, mc.ffn_inter_dim, mc.num_q_heads, mc.num_kv_heads, mc.head_dim
+        g = torch.Generator(device=dev).manual_seed(seed + 11)
+
+        def rnd(*shape, scale=0.02):
+            return (torch.randn(shape, device=dev, generator=g) * scale).half()
+        layers = [dict(wqkv=rnd((hq + 2 * hkv) * d, H), wo=rnd(H, hq * d), wug=rnd(2 * I, H), wd=rnd(H, I),
+                       n_in=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                       n_post=(torch.rand(H, device=dev, generator=g) + 0.5).half(),
+                       q_norm=(torch.rand(d, device=dev, generator=g) + 0.5).half(),
+                       k_norm=(torch.rand(d, device=dev, generator=g) + 0.5).half()) for _ in range(n_layers)]
+        weight_bytes = sum(t.numel() * 2 for t in layers[0].values())
+        stack = DecoderStack(mc, layers)
+        x = rnd(w.rows, H, scale=1.0)
+        res = torch.zeros_like(x)
+
+        def fwd():
+            stack.forward(x, res, w.k_cache, w.v_cache, w.block_table, ec, st, cos, sin)
+        us, per = _time_graph(fwd, torch.cuda.Stream(), reps, 2)
+        per = np.array(per) / n_layers
+        kv = w.algorithmic_bytes()
+        out[name] = {"rows": w.rows, "us_per_layer": us / n_layers,
+                     "us_per_layer_p10_p50_p90": [float(np.percentile(per, q)) for q in (10, 50, 90)],
+                     "weight_bytes_per_layer": weight_bytes, "kv_bytes_per_layer": kv,
+                     "gbps": (weight_bytes + (kv or 0)) / (us / n_layers) / 1e3}
+        stack.close()
+        del w, layers, stack, x, res
+        torch.cuda.empty_cache()
+    return out
+
+
 def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
     """The rest of the layer around the attention path, each kernel beside the
     reference's formulation on the same GPU (median of `reps` event-timed
@@ -680,6 +736,10 @@ def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
       3072 x 2 x 1024), beside the library GEMM then this build's
       SiLU-and-mul and the reference's torch formulation; algorithmic bytes =
       the stacked weight, read once;
+    * the q/k/v, O and down projections (the layer's F.linear calls) through
+      this build's split-k GEMM (fp32 split partials, which the next kernel
+      of the layer sums) beside torch.mm (hipBLASLt), at both batches;
+      algorithmic bytes = the weight, read once;
     * fused add-RMSNorm (rmsnorm.py:39-89) and SiLU-and-mul
       (silu_and_mul.py:5-34) at the verify batch (80 tokens) and a prefill
       chunk (8,192 tokens), Qwen3-8B widths; algorithmic bytes = every element
@@ -795,6 +855,43 @@ def measure_layer_rest(seed: int, reps: int = 50, cpu_seconds: float = 0.0):
                      "roofline": {"bound": "hbm", "achieved": nbytes / ours_graph / 1e3, "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": nbytes / ours_graph / 1e3 / HBM_PEAK_GBPS}}
         del ws, x, h, ug
+    torch.cuda.empty_cache()
+    from nebulasd_amd.kernels import linear_partials, linear_splits, sum_partials
+
+    for name, rows, n_out, n_in in (("proj_qkv_target_verify", 80, 6144, 4096),
+                                    ("proj_o_target_verify", 80, 4096, 4096),
+                                    ("proj_down_target_verify", 80, 4096, 12288),
+                                    ("proj_qkv_draft_decode", 64, 4096, 1024),
+                                    ("proj_o_draft_decode", 64, 1024, 2048),
+                                    ("proj_down_draft_decode", 64, 1024, 3072)):
+        # weight sets used in turn, together past the 256 MB MALL
+        nbytes = n_out * n_in * 2
+        n_sets = max(2, -(-600_000_000 // nbytes))
+        ws = [(torch.randn(n_out, n_in, device=dev, generator=g) * 0.03).half() for _ in range(n_sets)]
+        x = torch.randn(rows, n_in, device=dev, generator=g).half()
+        splits = linear_splits(rows, n_out, n_in)
+        part = torch.empty((splits, rows, n_out), device=dev, dtype=torch.float32)
+        y = torch.empty((rows, n_out), device=dev, dtype=torch.float16)
+        wturn = itertools.cycle(range(n_sets))
+
+        def ours_proj():
+            linear_partials(x, ws[next(wturn)], part)
+
+        def lib_proj():  # F.linear (hipBLASLt), as the reference's linear()
+            torch.mm(x, ws[next(wturn)].t(), out=y)
+        ours = timed(ours_proj)
+        lib = timed(lib_proj)
+        ours_graph = graph_us(ours_proj, calls=n_sets)
+        lib_graph = graph_us(lib_proj, calls=n_sets)
+        diff = float((sum_partials(linear_partials(x, ws[0])).float() - F.linear(x, ws[0]).float()).abs().max())
+        out[name] = {"rows": rows, "n_out": n_out, "n_in": n_in, "splits": splits, "us_per_call": ours,
+                     "us_per_call_graph": ours_graph, "library_us_per_call": lib,
+                     "library_us_per_call_graph": lib_graph, "speedup_vs_library_graph": lib_graph / ours_graph,
+                     "partial_bytes": splits * rows * n_out * 4, "hbm_gbps": nbytes / ours_graph / 1e3,
+                     "max_abs_diff_vs_library": diff,
+                     "roofline": {"bound": "hbm", "achieved": nbytes / ours_graph / 1e3, "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": nbytes / ours_graph / 1e3 / HBM_PEAK_GBPS}}
+        del ws, x, part, y
     torch.cuda.empty_cache()
     hidden, inter = 4096, 12288
     for tokens in (80, 8192):
@@ -1205,6 +1302,10 @@ def main():
     if args.layer_step:
         measure_layer_step.copy_gbps = copy_gbps
         r2 = measure_layer_step(args.seed)
+        r2["native_decoder_stack"] = nat = measure_native_layers(args.seed)
+        print("# native decoder stack: target verify %.1f us/layer (%d rows), draft decode %.1f us/layer (%d rows)"
+              % (nat["target_verify"]["us_per_layer"], nat["target_verify"]["rows"],
+                 nat["draft_decode"]["us_per_layer"], nat["draft_decode"]["rows"]), file=sys.stderr, flush=True)
         print("# target verify layer: %.1f us (three q/k/v GEMMs %.1f; library up/gate GEMM + SiLU-mul %.1f; "
               "GEMMs alone %.1f, rest alone %.1f; floor %s us)"
               % (r2["us_per_layer"], r2["us_per_layer_three_qkv_gemms"], r2["us_per_layer_unfused_ffn"],
@@ -1229,6 +1330,9 @@ def main():
                   r2["fused_add_rmsnorm_8192_tokens"]["reference_us_per_call"],
                   r2["silu_and_mul_8192_tokens"]["us_per_call"],
                   r2["silu_and_mul_8192_tokens"]["reference_us_per_call"]), file=sys.stderr, flush=True)
+        print("# projections (split-k / torch.mm, graph us): " + "; ".join(
+            f"{n[5:]} {r2[n]['us_per_call_graph']:.1f} / {r2[n]['library_us_per_call_graph']:.1f}"
+            for n in r2 if n.startswith("proj_")), file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     if args.hostkv:
         r2 = measure_hostkv(args.seed)
