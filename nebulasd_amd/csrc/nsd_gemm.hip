@@ -31,6 +31,7 @@
 // 6144 15.5 (23.2); Qwen3-0.6B at 64 rows, q/k/v 5.4 (11.6), O 4.2 (10.6),
 // down 4.9 (9.3).
 #include <algorithm>
+#include <atomic>
 
 #include "nsd_device.h"
 
@@ -222,11 +223,24 @@ LinearConfig choose_linear(int64_t n, int64_t k, int cus) {
   return best;
 }
 
+// Compute units of the current device (queried once per device: the
+// decoder stack asks for every projection it enqueues).
 int device_cus(int* cus) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *cus = c;
+      return NSD_OK;
+    }
+  }
   if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return fail(NSD_ERR_HIP, "linear: %s", hipGetErrorString(e));
+  if (*cus < 1) return fail(NSD_ERR_HIP, "linear: device %d reports %d compute units", dev, *cus);
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(*cus, std::memory_order_relaxed);
   return NSD_OK;
 }
 
