@@ -12,6 +12,13 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The FFN's up/gate projection + SiLU-and-mul through the split-k GEMM's
+// gated unit (nsd_gemm.hip), for shapes whose units fill the device (one
+// unit per 48 output columns, <= 112 rows); *served is false (and nothing is
+// launched) for the others.  Arguments as nsd_up_gate_silu_and_mul.
+int up_gate_silu_gated(const void* x, const void* up_gate, void* y, int64_t n_rows, int64_t hidden, int64_t inter,
+                       void* stream, bool* served);
+
 // Plan word layout (int32), shared by the planner and the attention launch.
 enum PlanHeader {
   kPlanMagic = 0,      // 0x4E534450

@@ -59,39 +59,53 @@ __device__ inline void gemm_wait() {
 }
 __device__ inline void gemm_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int MT, int TN>
+// GATED: the FFN's up/gate projection with SiLU-and-mul in the epilogue:
+// the unit's TN weight rows are TN/2 up rows then the same TN/2 gate rows
+// (W = [up; gate], 2 * n rows), over all of k, and the unit writes fp16
+// h = fp16(up) * fp16(silu(fp16(gate))) for its TN/2 columns.
+//
+// How the four waves share a step's MFMAs (kMode): 0 -- each wave one of the
+// four 32-k sub-steps over every output tile, summed across waves in LDS at
+// the end (TN 16, 32); 1 -- each wave TN/64 of the 16-column tiles over the
+// whole step (TN >= 64); 2 -- GATED: wave w (< TN/32) the up tile w and its
+// gate tile over the whole step, so the SiLU-and-mul needs no exchange.
+template <int MT, int TN, bool GATED = false>
 struct LinearShape {
   static constexpr int kRows = TN + 16 * MT;            // rows of one slot: weight, then x
   static constexpr int kSlot = kRows * kStepRowBytes;
   static constexpr int kRing = 3 * kSlot <= kGemmLds ? 3 : 2;
   static constexpr int kLds = kRing * kSlot;
   static constexpr int kDmaPerWave = kRows / 16;        // 4 rows per instruction, 4 waves
-  static constexpr bool kSplitN = TN >= 64;
+  static constexpr int kMode = GATED ? 2 : TN >= 64 ? 1 : 0;
   static_assert(kRing * kSlot <= kGemmLds, "ring");
-  static_assert(kSplitN || 4 * (TN / 16) * MT * 1024 <= kLds, "reduction buffer");
+  static_assert(kMode != 0 || 4 * (TN / 16) * MT * 1024 <= kLds, "reduction buffer");
+  static_assert(kMode != 2 || (TN / 32 <= 4 && TN % 32 == 0), "one up/gate tile pair per wave");
 };
 
 // Unit u = (n-tile u % n_tiles, split u / n_tiles); split s covers steps
 // [s T / splits, (s+1) T / splits) of the T = k / 128 steps.
-template <int MT, int TN>
+template <int MT, int TN, bool GATED = false>
 __global__ __launch_bounds__(kGemmThreads) void linear_partials_kernel(const f16* __restrict__ x,
                                                                        const f16* __restrict__ w,
                                                                        float* __restrict__ part, int rows,
                                                                        int n, int k, int splits,
-                                                                       int n_tiles) {
-  using S = LinearShape<MT, TN>;
+                                                                       int n_tiles, f16* __restrict__ y) {
+  using S = LinearShape<MT, TN, GATED>;
   constexpr int R = S::kRing;
   constexpr int NI = S::kDmaPerWave;
   constexpr int NJ = TN / 16;
-  constexpr int NJW = S::kSplitN ? NJ / 4 : NJ;  // n-tiles per wave
-  constexpr int KSUB = S::kSplitN ? 4 : 1;       // 32-k sub-steps per wave per step
+  constexpr int M = S::kMode;
+  constexpr int NJW = M == 1 ? NJ / 4 : M == 2 ? 2 : NJ;  // n-tiles per wave
+  constexpr int KSUB = M == 0 ? 1 : 4;                     // 32-k sub-steps per wave per step
   extern __shared__ __align__(16) char smem_raw[];
   lds_char* ring = (lds_char*)smem_raw;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const int nt = blockIdx.x % n_tiles, split = blockIdx.x / n_tiles;
-  const int n0 = nt * TN;
+  const int n0 = nt * (GATED ? TN / 2 : TN);
+  const bool computes = M != 2 || wave < NJ / 2;
+  auto tile_of = [&](int j) { return M == 1 ? wave * NJW + j : M == 2 ? wave + j * (NJ / 2) : j; };
   const int T = k / kKStep;
   const int t0 = (int)((int64_t)split * T / splits);
   const int steps = (int)((int64_t)(split + 1) * T / splits) - t0;
@@ -103,7 +117,9 @@ __global__ __launch_bounds__(kGemmThreads) void linear_partials_kernel(const f16
   for (int i = 0; i < NI; ++i) {
     const int row = (4 * i + wave) * 4 + (lane >> 4);
     const int chunk = (lane & 15) ^ chunk_swizzle(row);
-    const f16* base = row < TN ? w + (int64_t)(n0 + row) * k
+    // weight row of slot row `row` (GATED: up rows, then the gate rows n further on)
+    const int wrow = !GATED || row < TN / 2 ? n0 + row : n + n0 + row - TN / 2;
+    const f16* base = row < TN ? w + (int64_t)wrow * k
                                : x + (int64_t)(row - TN < rows ? row - TN : rows - 1) * k;  // pad rows: a real row
     src[i] = base + (int64_t)t0 * kKStep + chunk * 8;
   }
@@ -129,13 +145,14 @@ __global__ __launch_bounds__(kGemmThreads) void linear_partials_kernel(const f16
     gemm_barrier();
     if (issued < steps) issue(issued++);
     const lds_char* sl = ring + (t % R) * S::kSlot;
+    if (!computes) continue;
 #pragma unroll
     for (int kk = 0; kk < KSUB; ++kk) {
-      const int ch = 4 * (S::kSplitN ? kk : wave) + lg;  // lane group's 8 k of the sub-step
+      const int ch = 4 * (M == 0 ? wave : kk) + lg;  // lane group's 8 k of the sub-step
       f16x8 a[NJW], b[MT];
 #pragma unroll
       for (int j = 0; j < NJW; ++j) {
-        const int row = 16 * ((S::kSplitN ? wave * NJW : 0) + j) + lr;
+        const int row = 16 * tile_of(j) + lr;
         a[j] = *(const lds_f16x8*)(sl + row * kStepRowBytes + ((ch ^ chunk_swizzle(row)) << 4));
       }
 #pragma unroll
@@ -156,11 +173,29 @@ __global__ __launch_bounds__(kGemmThreads) void linear_partials_kernel(const f16
     const int m = 16 * i + lr;
     if (m < rows) *reinterpret_cast<f32x4*>(out + (int64_t)m * n + n0 + 16 * j + 4 * lg) = v;
   };
-  if constexpr (S::kSplitN) {
+  if constexpr (M == 1) {
 #pragma unroll
     for (int j = 0; j < NJW; ++j)
 #pragma unroll
-      for (int i = 0; i < MT; ++i) store(wave * NJW + j, i, acc[j][i]);
+      for (int i = 0; i < MT; ++i) store(tile_of(j), i, acc[j][i]);
+  } else if constexpr (M == 2) {
+    // up tile `wave` and its gate tile leave the same lane layout: the
+    // SiLU-and-mul of silu_and_mul_kernel on the fp16-rounded sums
+    if (!computes) return;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int m = 16 * i + lr;
+      if (m >= rows) continue;
+      f16x4 h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16 up = (f16)acc[0][i][e];
+        const float gf = (float)(f16)acc[1][i][e];
+        const f16 sg = (f16)(gf / (1.f + expf(-gf)));
+        h[e] = (f16)((float)up * (float)sg);
+      }
+      *reinterpret_cast<f16x4*>(y + (int64_t)m * n + n0 + 16 * wave + 4 * lg) = h;
+    }
   } else {
     __syncthreads();  // the ring is drained: its LDS holds the waves' sums
     f32x4* red = reinterpret_cast<f32x4*>(smem_raw);  // [wave][tile][lane]
@@ -265,8 +300,37 @@ int launch_linear(const f16* x, const f16* w, float* part, int rows, int n, int 
   }
   const int n_tiles = n / TN;
   hipLaunchKernelGGL((linear_partials_kernel<MT, TN>), dim3(n_tiles * splits), dim3(kGemmThreads), S::kLds, st, x,
-                     w, part, rows, n, k, splits, n_tiles);
+                     w, part, rows, n, k, splits, n_tiles, nullptr);
   return launch_status("linear");
+}
+
+// The gated (up/gate + SiLU-and-mul) unit: 48 up and 48 gate columns over
+// all of k, one unit per 48 output columns.
+constexpr int kGatedTile = 96;
+constexpr int kGatedMaxRowTiles = 7;  // three ring slots fit up to 112 rows (128 rows: the ring kernel, 1.5 us faster)
+
+template <int MT>
+int launch_gated(const f16* x, const f16* w, f16* y, int rows, int inter, int hidden, hipStream_t st) {
+  using S = LinearShape<MT, kGatedTile, true>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_partials_kernel<MT, kGatedTile, true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
+    if (e != hipSuccess) return fail(NSD_ERR_HIP, "up_gate: LDS attribute: %s", hipGetErrorString(e));
+    attr_set = true;
+  }
+  const int n_tiles = inter / (kGatedTile / 2);
+  hipLaunchKernelGGL((linear_partials_kernel<MT, kGatedTile, true>), dim3(n_tiles), dim3(kGemmThreads), S::kLds, st,
+                     x, w, nullptr, rows, inter, hidden, 1, n_tiles, y);
+  return launch_status("up_gate_silu_and_mul");
+}
+
+template <int... I>
+int launch_gated_rows(std::integer_sequence<int, I...>, int mt, const f16* x, const f16* w, f16* y, int rows,
+                      int inter, int hidden, hipStream_t st) {
+  int rc = NSD_ERR_UNSUPPORTED;
+  ((mt == I + 1 ? (rc = launch_gated<I + 1>(x, w, y, rows, inter, hidden, st), 0) : 0), ...);
+  return rc;
 }
 
 template <int TN, int... I>
@@ -278,6 +342,24 @@ int launch_linear_rows(std::integer_sequence<int, I...>, int mt, const f16* x, c
 }
 
 }  // namespace
+
+int up_gate_silu_gated(const void* x, const void* up_gate, void* y, int64_t n_rows, int64_t hidden, int64_t inter,
+                       void* stream, bool* served) {
+  *served = false;
+  int cus = 0;
+  if (int rc = device_cus(&cus)) return rc;
+  const int64_t units = inter / (kGatedTile / 2);
+  // one unit per CU or close to it (fewer units leave CUs idle: the older
+  // kernel spreads small shapes better)
+  if (inter % (kGatedTile / 2) || units * 10 < cus * 9 || units > cus || n_rows > 16 * kGatedMaxRowTiles ||
+      hidden % kKStep)
+    return NSD_OK;
+  *served = true;
+  return launch_gated_rows(std::make_integer_sequence<int, kGatedMaxRowTiles>{}, (int)((n_rows + 15) / 16),
+                           static_cast<const f16*>(x), static_cast<const f16*>(up_gate), static_cast<f16*>(y),
+                           (int)n_rows, (int)inter, (int)hidden, as_stream(stream));
+}
+
 }  // namespace nsd
 
 using namespace nsd;

@@ -661,6 +661,9 @@ extern "C" int nsd_up_gate_silu_and_mul(const void* x, const void* up_gate, void
     return fail(NSD_ERR_UNSUPPORTED, "up_gate_silu_and_mul: inter=%lld (need a multiple of 16)", (long long)inter);
   if (!aligned16(x) || !aligned16(up_gate) || !aligned16(y))
     return fail(NSD_ERR_UNSUPPORTED, "up_gate_silu_and_mul: pointers must be 16-byte aligned");
+  bool served = false;
+  if (int rc = up_gate_silu_gated(x, up_gate, y, n_rows, hidden, inter, stream, &served)) return rc;
+  if (served) return NSD_OK;
   const hipStream_t s = as_stream(stream);
   const int n_tiles = (int)(inter / 16);
   const int grid = std::min(rg_grid(), n_tiles);

@@ -72,7 +72,8 @@ def test_silu_and_mul_matches_oracle(gpu, rows, inter):
     print(f"silu_and_mul {rows}x{inter}: exact {exact:.4f}", flush=True)
 
 
-@pytest.mark.parametrize("rows,hidden,inter", [(1, 4096, 12288), (80, 4096, 12288), (64, 1024, 3072),
+@pytest.mark.parametrize("rows,hidden,inter", [(1, 4096, 12288), (80, 4096, 12288), (97, 4096, 12288),
+                                               (128, 4096, 12288), (64, 1024, 3072),
                                                (129, 1024, 3072), (33, 256, 4800), (16, 128, 16),
                                                (20, 512, 28672)])
 def test_up_gate_silu_and_mul_matches_oracle(gpu, rows, hidden, inter):
@@ -81,7 +82,9 @@ def test_up_gate_silu_and_mul_matches_oracle(gpu, rows, hidden, inter):
     199-200), and against the library GEMM then this build's SiLU-and-mul.
     Shapes: the Qwen3-8B verify and Qwen3-0.6B draft batches, one row, two
     passes of rows (129), output tiles not a multiple of the CU count (300),
-    one tile, and more tiles per workgroup than one group holds (7 of 6).
+    one tile, and more tiles per workgroup than one group holds (7 of 6);
+    the Qwen3-8B shape (one 48-column unit per CU) takes the split-k GEMM's
+    gated unit at 1, 80 and 97 rows (up to 112), the ring kernel at 128.
     Rows past the output are never written."""
     x = _randn(gpu, rows, hidden, seed=11)
     w = _randn(gpu, 2 * inter, hidden, seed=12, scale=0.03)
