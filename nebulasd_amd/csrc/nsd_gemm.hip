@@ -23,7 +23,10 @@
 //     each wave owns TN/64 of the 16-column n-tiles over the whole step, for
 //     TN = 16 and 32 each wave owns one of the step's four 32-k sub-steps
 //     over every output tile and the four waves' sums are added in LDS, in
-//     wave order, at the end.
+//     wave order, at the end;
+//   - a gated unit serves the FFN's up/gate projection: 48 up and the
+//     matching 48 gate rows over all of k, the SiLU-and-mul applied to the
+//     accumulators, fp16 output (no partials).
 //
 // Measured on MI355X against hipBLASLt (the library F.linear uses), µs per
 // call with the weights rotated past the MALL: Qwen3-8B at 80 rows, O
@@ -167,8 +170,8 @@ __global__ __launch_bounds__(kGemmThreads) void linear_partials_kernel(const f16
     }
   }
   // lane (lg, lr) holds columns 4lg .. 4lg+3 of an n-tile for row lr of an
-  // m-tile: 16 contiguous bytes of the partial row
-  float* out = part + (int64_t)split * rows * n;
+  // m-tile: 16 contiguous bytes of the partial row (no partials when gated)
+  float* out = GATED ? nullptr : part + (int64_t)split * rows * n;
   auto store = [&](int j, int i, f32x4 v) {
     const int m = 16 * i + lr;
     if (m < rows) *reinterpret_cast<f32x4*>(out + (int64_t)m * n + n0 + 16 * j + 4 * lg) = v;
