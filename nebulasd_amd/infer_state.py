@@ -84,6 +84,19 @@ def reference_seq_block_size(num_kv_heads: int, decoding_seq_lens_list) -> int:
     return sbs
 
 
+def host_to_device(values, dtype, device) -> torch.Tensor:
+    """A device tensor of host values without synchronising the host: the
+    values are copied into pinned memory (torch's caching host allocator
+    keeps the block until the copy has run) and sent with a non-blocking
+    copy on the current stream.  (``torch.tensor(values, device=cuda)``
+    waits for the stream: every kernel enqueued before it must finish.)"""
+    dev = torch.device(device)
+    t = torch.tensor(values, dtype=dtype)
+    if dev.type != "cuda":
+        return t.to(dev)
+    return t.pin_memory().to(dev, non_blocking=True)
+
+
 def build_infer_state(seq_ids_list, decoding_seq_lens_list, prefill_lens_list, model_config,
                       cos_cache: torch.Tensor, sin_cache: torch.Tensor, device,
                       max_group_rows: int = 0, ignore_kvcache: bool = False) -> LlamaInferState:
@@ -100,24 +113,24 @@ def build_infer_state(seq_ids_list, decoding_seq_lens_list, prefill_lens_list, m
     if len(seq_ids_list) != num_prefill + len(decoding_seq_lens_list):
         raise ValueError("seq_ids_list must list prefill sequences then decode rows")
     dev = torch.device(device)
-    i32 = dict(dtype=torch.int32, device=dev)
+    i32 = torch.int32
     num_tokens = sum(prefill_lens_list) + len(decoding_seq_lens_list)
-    prefill_lens = torch.tensor(prefill_lens_list, **i32)
+    prefill_lens = host_to_device(prefill_lens_list, i32, dev)
     starts = torch.cumsum(prefill_lens, 0, dtype=torch.int32) - prefill_lens
-    dec_lens = torch.tensor(decoding_seq_lens_list, **i32)
+    dec_lens = host_to_device(decoding_seq_lens_list, i32, dev)
     positions = [p for n in prefill_lens_list for p in range(n)] + [s - 1 for s in decoding_seq_lens_list]
-    pos = torch.tensor(positions, dtype=torch.long, device=dev)
+    pos = host_to_device(positions, torch.long, dev)
     max_dec = max(decoding_seq_lens_list) if decoding_seq_lens_list else 0
     sbs = reference_seq_block_size(model_config.num_kv_heads, decoding_seq_lens_list)
     return LlamaInferState(
         batch_size=len(seq_ids_list),
         num_tokens=num_tokens,
-        seq_ids=torch.tensor(seq_ids_list, **i32),
+        seq_ids=host_to_device(seq_ids_list, i32, dev),
         softmax_scale=model_config.head_dim ** -0.5,
         num_prefill_seqs=num_prefill,
         num_prefill_tokens=num_tokens - len(decoding_seq_lens_list),
         prefill_seq_start_locs=starts,
-        prefill_seq_start_locs_with_end=torch.cat([starts, torch.tensor([num_tokens], **i32)]),
+        prefill_seq_start_locs_with_end=torch.cat([starts, host_to_device([num_tokens], i32, dev)]),
         prefill_seq_lens=prefill_lens,
         max_prefill_len=max(prefill_lens_list) if prefill_lens_list else 0,
         num_decoding_seqs=len(decoding_seq_lens_list),

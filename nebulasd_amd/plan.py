@@ -159,7 +159,11 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
         words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim,
                                block_size, bt_rows, bt_stride,
                                num_workers(rows_max, device.index), max_group_rows)
-    dev = torch.from_numpy(words).to(device, non_blocking=False)
+    # pinned and non-blocking: the upload does not wait for the stream
+    # (the caching host allocator keeps the pinned block until the copy ran)
+    src = torch.from_numpy(words)
+    dev = (src.pin_memory().to(device, non_blocking=True) if device.type == "cuda"
+           else src.to(device))
     # the split segments' partials; every launch writes each slot before
     # the merge reads it, so the buffer needs no initialisation
     workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=device)

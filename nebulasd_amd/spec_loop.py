@@ -50,7 +50,7 @@ import torch
 import torch.nn.functional as F
 
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
-from .infer_state import build_infer_state, model_rope_cache
+from .infer_state import build_infer_state, host_to_device, model_rope_cache
 from .kernels import (FUSED_UP_GATE_MAX_ROWS, flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention,
                       post_layer_forward, qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace,
                       silu_and_mul_inplace, store_kvcache, up_gate_silu_and_mul)
@@ -110,15 +110,23 @@ class RandomQwen3:
         self.native = native
         self.stack = None  # the native decoder stack, built on first use
 
-    def _forward(self, st, token_ids: list, attention) -> list:
+    def _token_tensor(self, tokens) -> torch.Tensor:
+        """Token ids as a device int64 tensor (a device tensor passes through;
+        a host list is sent without waiting for the stream)."""
+        if isinstance(tokens, torch.Tensor):
+            return tokens
+        return host_to_device(tokens, torch.long, self.dev)
+
+    def _forward(self, st, token_ids, attention, as_tensor: bool = False):
         """transformer_layer.py:83-201 for every layer, then model.py:292 and
         the post-layer (post_layer.py:49-79); `attention(li, lw, q, k, v)`
         returns o [tokens, Hq, d].  Returns the greedy token of every request
-        (every prompt's last token, then every decode row)."""
+        (every prompt's last token, then every decode row): a list, or with
+        ``as_tensor`` the int64 device tensor (no host synchronisation)."""
         mc, dev = self.mc, self.dev
         eps, inter = mc.rms_norm_eps, mc.ffn_inter_dim
         hq, hkv, d = mc.num_q_heads, mc.num_kv_heads, mc.head_dim
-        x = self.embed[torch.tensor(token_ids, device=dev)]
+        x = self.embed[self._token_tensor(token_ids)]
         res = torch.zeros_like(x)
         for li, lw in enumerate(self.layers):
             fused_add_rmsnorm_inplace(x, res, lw["n_in"], eps)
@@ -141,7 +149,8 @@ class RandomQwen3:
                 x = F.linear(h, lw["wd"])
         x += res
         with forward_phase_range("post_lm_head"):
-            return post_layer_forward(x, st, self.final_norm, self.lm_head, eps).tolist()
+            out = post_layer_forward(x, st, self.final_norm, self.lm_head, eps)
+        return out if as_tensor else out.tolist()
 
     def prefill(self, seq_ids: list, prompts: list, ignore_kvcache: bool = False) -> list:
         """Run the prompts; returns each one's greedy next token.  With
@@ -166,13 +175,15 @@ class RandomQwen3:
                                           st.max_prefill_len, softmax_scale=st.softmax_scale)
         return self._forward(st, [t for p in prompts for t in p], attention)
 
-    def decode(self, seq_ids: list, seq_lens: list, tokens: list) -> list:
+    def decode(self, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False):
         """Decode / verify rows (rows of one sequence contiguous, seq_lens
-        rising by one); returns the greedy next token of every row."""
+        rising by one); returns the greedy next token of every row.  `tokens`
+        is a host list or an int64 device tensor; with ``as_tensor`` the result
+        stays on the device (no host synchronisation)."""
         mc, dev = self.mc, self.dev
         st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
         if self.native and len(tokens) <= DECODER_MAX_ROWS and not PHASE_RANGES:
-            return self._decode_native(st, seq_ids, seq_lens, tokens)
+            return self._decode_native(st, seq_ids, seq_lens, tokens, as_tensor)
         hq = mc.num_q_heads
 
         def attention(li, lw, q_rows, k, v):
@@ -193,16 +204,16 @@ class RandomQwen3:
                     paged_attention(q, self.k_cache, self.v_cache, self.block_table, mc, self.ec, st,
                                     li, o)
             return o
-        return self._forward(st, tokens, attention)
+        return self._forward(st, tokens, attention, as_tensor)
 
-    def _decode_native(self, st, seq_ids: list, seq_lens: list, tokens: list) -> list:
+    def _decode_native(self, st, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False):
         """decode() with every layer in one call of the native decoder stack;
         a sampled attention check receives its layer's q, o and LSE after
         the forward (later layers write only their own cache slots)."""
         mc, dev = self.mc, self.dev
         if self.stack is None:
             self.stack = DecoderStack(mc, self.layers)
-        x = self.embed[torch.tensor(tokens, device=dev)]
+        x = self.embed[self._token_tensor(tokens)]
         res = torch.zeros_like(x)
         probe_layer = self.check[0] if self.check is not None else -1
         probe = self.stack.forward(x, res, self.k_cache, self.v_cache, self.block_table, self.ec, st, self.cos,
@@ -213,7 +224,8 @@ class RandomQwen3:
             self.check = None
         x += res
         with forward_phase_range("post_lm_head"):
-            return post_layer_forward(x, st, self.final_norm, self.lm_head, mc.rms_norm_eps).tolist()
+            out = post_layer_forward(x, st, self.final_norm, self.lm_head, mc.rms_norm_eps)
+        return out if as_tensor else out.tolist()
 
 
 def _sync(dev: torch.device) -> None:
@@ -224,7 +236,7 @@ def _sync(dev: torch.device) -> None:
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
         target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
         draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, share_weights=False, return_outputs=False,
-        log=None, native=True) -> dict:
+        log=None, native=True, sync_each_forward=False) -> dict:
     """The speculative loop over `n_requests` synthetic requests; returns a summary.
 
     With ``check_every`` > 0, every check_every-th forward calls
@@ -236,6 +248,14 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     the draft's two-row reconcile step, which independent random models
     (acceptance 0) never reach.  ``return_outputs`` adds every request's
     generated tokens to the summary (key ``outputs``).
+
+    A draft group's forwards are enqueued back to back: the draft's
+    proposals stay on the device (each step's tokens are the next step's
+    input), the target batches read them there, and the host reads the
+    proposals and the target's tokens back once per draft group, so it
+    builds the next forward's metadata while the GPU runs the previous one.
+    ``sync_each_forward`` waits for every forward instead (same results:
+    the kernels are deterministic; for tests and timing comparisons).
     """
     dev = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -278,10 +298,11 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
         stats["rounds"] += 1
         for ds in range(0, len(live), draft_batch):
             dgroup = live[ds:ds + draft_batch]
-            # draft: `depth` proposals per request
-            props = {r: [] for r in dgroup}
+            # draft: `depth` proposals per request, kept on the device; step
+            # j's tokens in request order ([len(dgroup)] int64)
+            steps_dev = []
             for j in range(depth):
-                sids, slens, toks, last_row = [], [], [], {}
+                sids, slens, toks, last_row = [], [], [], []
                 for r in dgroup:
                     base = plens[r] + len(out[r]) - 1 + j  # tokens before this step's input
                     if j == 0 and draft_missing[r] is not None:
@@ -292,34 +313,49 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                     else:
                         sids.append(r)
                         slens.append(base + 1)
-                        toks.append(out[r][-1] if j == 0 else props[r][-1])
-                    last_row[r] = len(toks) - 1
+                        if j == 0:
+                            toks.append(out[r][-1])
+                    last_row.append(len(sids) - 1)
+                if j > 0:  # one row per request: the previous step's proposals
+                    toks = steps_dev[-1]
                 if check_every and make_check and step % check_every == 0:
                     draft.check = (draft.mc.num_layers // 2, make_check())
                     n_checks += 1
                 step += 1
-                nxt = draft.decode(sids, slens, toks)
+                nxt = draft.decode(sids, slens, toks, as_tensor=True)
                 stats["draft_forwards"] += 1
-                for r in dgroup:
-                    props[r].append(nxt[last_row[r]])
-                    if j == 0:
-                        draft_missing[r] = None
-            # target: verify each target batch
+                if sync_each_forward:
+                    _sync(dev)
+                steps_dev.append(nxt if len(sids) == len(dgroup)
+                                 else nxt[host_to_device(last_row, torch.long, dev)])
+            for r in dgroup:
+                draft_missing[r] = None
+            # target: verify each target batch, rows [anchor, proposals...] per request
+            anchors = host_to_device([out[r][-1] for r in dgroup], torch.long, dev)
+            props_dev = torch.stack(steps_dev, 1)
+            rows_dev = torch.cat([anchors[:, None], props_dev], 1)
+            posts = []
             for ts in range(0, len(dgroup), target_batch):
                 tgroup = dgroup[ts:ts + target_batch]
-                sids, slens, toks = [], [], []
+                sids, slens = [], []
                 for r in tgroup:
                     base = plens[r] + len(out[r]) - 1
-                    rows = [out[r][-1], *props[r]]
-                    sids += [r] * len(rows)
-                    slens += list(range(base + 1, base + 1 + len(rows)))
-                    toks += rows
+                    sids += [r] * (depth + 1)
+                    slens += list(range(base + 1, base + 2 + depth))
                 if check_every and make_check and step % check_every == 0:
                     target.check = (target.mc.num_layers // 2, make_check())
                     n_checks += 1
                 step += 1
-                post = target.decode(sids, slens, toks)
+                posts.append((tgroup, target.decode(sids, slens, rows_dev[ts:ts + len(tgroup)].reshape(-1),
+                                                    as_tensor=True)))
                 stats["target_forwards"] += 1
+                if sync_each_forward:
+                    _sync(dev)
+            # one read-back per draft group: the proposals, then each batch's tokens
+            props_host = props_dev.tolist()
+            props = {r: props_host[i] for i, r in enumerate(dgroup)}
+            for tgroup, post_dev in posts:
+                post = post_dev.tolist()
                 for i, r in enumerate(tgroup):
                     p = post[i * (depth + 1):(i + 1) * (depth + 1)]
                     acc, n_acc = compute_greedy_acceptance(props[r], p, new_tokens - len(out[r]))

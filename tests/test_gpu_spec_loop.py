@@ -71,6 +71,22 @@ def test_speculative_loop_shared_weights_accepts(gpu):
     assert any(r["max_q_len"] == 2 and r["rows"] < 5 * 64 for r in results)
 
 
+def test_speculative_loop_pipelined_equals_synchronous(gpu):
+    """Forwards enqueued back to back with device-resident proposals give the
+    same tokens and counters as waiting for every forward (deterministic
+    kernels), with proposals accepted and two-row reconcile groups present."""
+    kw = dict(n_requests=24, prompt_lo=64, prompt_hi=400, new_tokens=12, draft_batch=16, target_batch=8,
+              depth=4, seed=8, device=gpu, share_weights=True, return_outputs=True)
+    a = run(**kw)
+    b = run(**kw, sync_each_forward=True)
+    print({k: v for k, v in a.items() if k != "outputs"}, flush=True)
+    assert a["reconcile_groups"] > 0 and a["accepted"] > 0
+    assert a["outputs"] == b["outputs"]
+    for key in ("accepted", "proposed", "reconcile_groups", "full_accepts", "partial_accepts", "rounds",
+                "target_forwards", "draft_forwards"):
+        assert a[key] == b[key], key
+
+
 def test_prefill_ignore_kvcache_leaves_cache(gpu):
     """A prefill forward with ignore_kvcache writes no cache slot and returns
     the same tokens (prefill attention reads k/v directly), as the reference's

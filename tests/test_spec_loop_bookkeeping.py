@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from nebulasd_amd import spec_loop
 from nebulasd_amd.config import QWEN3_8B, ModelConfig
@@ -63,7 +64,9 @@ class ScriptedModel:
             out.append(self._token(self.cache[r]))
         return out
 
-    def decode(self, seq_ids, seq_lens, tokens):
+    def decode(self, seq_ids, seq_lens, tokens, as_tensor=False):
+        if isinstance(tokens, torch.Tensor):  # the loop passes device-resident proposals
+            tokens = tokens.tolist()
         assert len(seq_ids) == len(seq_lens) == len(tokens)
         out = []
         for r, n, t in zip(seq_ids, seq_lens, tokens):
@@ -73,7 +76,7 @@ class ScriptedModel:
             del c[pos:]  # the row rewrites its position; later positions are stale
             c.append(int(t))
             out.append(self._token(c))
-        return out
+        return torch.tensor(out, dtype=torch.long) if as_tensor else out
 
 
 def target_continuations(n_requests, new_tokens):
