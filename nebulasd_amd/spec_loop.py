@@ -41,6 +41,7 @@ tests/run_spec_loop.py for the full 512-request configuration).
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import math
 import time
@@ -236,7 +237,7 @@ def _sync(dev: torch.device) -> None:
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
         target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
         draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, share_weights=False, return_outputs=False,
-        log=None, native=True, sync_each_forward=False) -> dict:
+        log=None, native=True, sync_each_forward=False, overlap=True) -> dict:
     """The speculative loop over `n_requests` synthetic requests; returns a summary.
 
     With ``check_every`` > 0, every check_every-th forward calls
@@ -256,6 +257,12 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     builds the next forward's metadata while the GPU runs the previous one.
     ``sync_each_forward`` waits for every forward instead (same results:
     the kernels are deterministic; for tests and timing comparisons).
+
+    ``overlap`` (on a GPU, without ``sync_each_forward``) runs the draft's
+    forwards on one stream and the target's on another, the target's waiting
+    for its group's proposals by an event, and reads a group's results back
+    after the next group is enqueued: the next group's draft forwards then
+    run beside this group's verifies.  Results are the same either way.
     """
     dev = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -291,13 +298,30 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
              "accepted": 0, "reconcile_groups": 0, "full_accepts": 0, "partial_accepts": 0,
              "multi_token_appends": 0}
     step = 0
-    while True:
-        live = [r for r in range(n_requests) if len(out[r]) < new_tokens]
-        if not live:
-            break
-        stats["rounds"] += 1
-        for ds in range(0, len(live), draft_batch):
-            dgroup = live[ds:ds + draft_batch]
+    # draft forwards on one stream, target verifies on another: a draft
+    # group's forwards run beside the previous group's verifies (other
+    # requests, the other model), as the reference's draft and target
+    # workers run side by side (streams at the default priority)
+    overlap = overlap and not sync_each_forward and dev.type == "cuda"
+    d_stream = torch.cuda.Stream(device=dev) if overlap else None
+    t_stream = torch.cuda.Stream(device=dev) if overlap else None
+
+    def on(stream):
+        return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
+    def to_host(t: torch.Tensor) -> torch.Tensor:
+        """Copy of `t` in pinned host memory, enqueued on the current stream."""
+        if t.device.type != "cuda":
+            return t
+        h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        h.copy_(t, non_blocking=True)
+        return h
+
+    def enqueue_group(dgroup: list):
+        """The group's draft proposals and target verifies, enqueued; returns
+        what finish_group reads back."""
+        nonlocal step, n_checks
+        with on(d_stream):
             # draft: `depth` proposals per request, kept on the device; step
             # j's tokens in request order ([len(dgroup)] int64)
             steps_dev = []
@@ -330,10 +354,19 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                                  else nxt[host_to_device(last_row, torch.long, dev)])
             for r in dgroup:
                 draft_missing[r] = None
-            # target: verify each target batch, rows [anchor, proposals...] per request
+            # target rows per request: [anchor, proposals...]
             anchors = host_to_device([out[r][-1] for r in dgroup], torch.long, dev)
             props_dev = torch.stack(steps_dev, 1)
             rows_dev = torch.cat([anchors[:, None], props_dev], 1)
+            drafted = torch.cuda.Event() if overlap else None
+            if overlap:
+                drafted.record(d_stream)
+        with on(t_stream):
+            if overlap:
+                t_stream.wait_event(drafted)
+                # made on the draft stream, read on this one
+                props_dev.record_stream(t_stream)
+                rows_dev.record_stream(t_stream)
             posts = []
             for ts in range(0, len(dgroup), target_batch):
                 tgroup = dgroup[ts:ts + target_batch]
@@ -352,23 +385,49 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                 if sync_each_forward:
                     _sync(dev)
             # one read-back per draft group: the proposals, then each batch's tokens
-            props_host = props_dev.tolist()
-            props = {r: props_host[i] for i, r in enumerate(dgroup)}
-            for tgroup, post_dev in posts:
-                post = post_dev.tolist()
-                for i, r in enumerate(tgroup):
-                    p = post[i * (depth + 1):(i + 1) * (depth + 1)]
-                    acc, n_acc = compute_greedy_acceptance(props[r], p, new_tokens - len(out[r]))
-                    stats["proposed"] += depth
-                    stats["accepted"] += n_acc
-                    stats["full_accepts"] += n_acc == depth
-                    # a proposal token rejected after at least one accepted (not a
-                    # proposal cut short by the output limit: len(acc) == n_acc then)
-                    stats["partial_accepts"] += 0 < n_acc < depth and len(acc) == n_acc + 1
-                    stats["multi_token_appends"] += len(acc) > 1
-                    if n_acc == depth and len(acc) == depth + 1:
-                        draft_missing[r] = props[r][-1]
-                    out[r] += acc
+            props_h = to_host(props_dev)
+            posts_h = [(tgroup, to_host(post)) for tgroup, post in posts]
+            done = torch.cuda.Event() if dev.type == "cuda" else None
+            if done is not None:
+                done.record()
+        return dgroup, props_h, posts_h, done
+
+    def finish_group(pending) -> None:
+        """Greedy acceptance of a group whose verifies were enqueued."""
+        dgroup, props_h, posts_h, done = pending
+        if done is not None:
+            done.synchronize()
+        props_host = props_h.tolist()
+        props = {r: props_host[i] for i, r in enumerate(dgroup)}
+        for tgroup, post_h in posts_h:
+            post = post_h.tolist()
+            for i, r in enumerate(tgroup):
+                p = post[i * (depth + 1):(i + 1) * (depth + 1)]
+                acc, n_acc = compute_greedy_acceptance(props[r], p, new_tokens - len(out[r]))
+                stats["proposed"] += depth
+                stats["accepted"] += n_acc
+                stats["full_accepts"] += n_acc == depth
+                # a proposal token rejected after at least one accepted (not a
+                # proposal cut short by the output limit: len(acc) == n_acc then)
+                stats["partial_accepts"] += 0 < n_acc < depth and len(acc) == n_acc + 1
+                stats["multi_token_appends"] += len(acc) > 1
+                if n_acc == depth and len(acc) == depth + 1:
+                    draft_missing[r] = props[r][-1]
+                out[r] += acc
+
+    while True:
+        live = [r for r in range(n_requests) if len(out[r]) < new_tokens]
+        if not live:
+            break
+        stats["rounds"] += 1
+        # group g's acceptance is read back after group g + 1 is enqueued
+        pending = None
+        for ds in range(0, len(live), draft_batch):
+            nxt_pending = enqueue_group(live[ds:ds + draft_batch])
+            if pending is not None:
+                finish_group(pending)
+            pending = nxt_pending
+        finish_group(pending)
         if log:
             log(f"round {stats['rounds']}: {sum(min(len(o), new_tokens) for o in out)} tokens")
     _sync(dev)
@@ -398,10 +457,12 @@ def main():
                    help="draft = the target's model and weights (proposals accepted)")
     p.add_argument("--python-layers", action="store_true",
                    help="run decode/verify layers from Python instead of the native decoder stack")
+    p.add_argument("--no-overlap", action="store_true",
+                   help="draft and target forwards on one stream (no draft/verify overlap)")
     a = p.parse_args()
     res = run(a.requests, a.prompt_lo, a.prompt_hi, a.new_tokens, a.draft_batch, a.target_batch,
               a.depth, a.seed, share_weights=a.share_weights, log=lambda m: print(m, flush=True),
-              native=not a.python_layers)
+              native=not a.python_layers, overlap=not a.no_overlap)
     print(json.dumps(res), flush=True)
 
 
