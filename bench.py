@@ -1138,15 +1138,18 @@ def measure_spec_loop(seed: int, steps: int, cpu_seconds: float) -> dict:
     out = {"workload": "spec_loop_shapes", "loop": {k: v for k, v in res.items()},
            "bench_wall_s": wall}
     thr = {}
-    for native in (True, False):
-        r = run(n_requests=64, prompt_lo=128, prompt_hi=1024, new_tokens=32, draft_batch=64, target_batch=16,
-                depth=4, seed=seed, device=dev, native=native)
-        thr["native_decoder_stack" if native else "python_layers"] = {
+    for name, native, overlap in (("native_decoder_stack", True, True), ("native_one_stream", True, False),
+                                  ("python_layers", False, True)):
+        r = run(n_requests=128, prompt_lo=128, prompt_hi=1024, new_tokens=32, draft_batch=64, target_batch=16,
+                depth=4, seed=seed, device=dev, native=native, overlap=overlap)
+        thr[name] = {
             "decode_tokens_per_s": r["decode_tokens_per_s"], "wall_s": r["wall_s"], "prefill_s": r["prefill_s"],
             "rounds": r["rounds"], "generated_tokens": r["generated_tokens"]}
         torch.cuda.empty_cache()
-    out["throughput"] = dict(thr, config="64 requests x 32 generated tokens, prompts U[128, 1024], draft batch 64, "
-                                         "target batch 16, depth 4, no sampled checks")
+    out["throughput"] = dict(thr, config="128 requests x 32 generated tokens, prompts U[128, 1024], draft batch 64 "
+                                         "(two draft groups per round), target batch 16, depth 4, no sampled "
+                                         "checks; draft and target forwards on two streams except "
+                                         "native_one_stream")
     for role, xs in samples.items():
         if not xs:
             continue
@@ -1358,9 +1361,10 @@ def main():
         r2 = measure_spec_loop(args.seed, args.steps, args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
         print("# speculative loop shapes: " + "; ".join(
             f"{role} {r2[role]['us_per_layer_call_median']:.1f} us/layer-call over {r2[role]['samples']} forwards"
-            for role in ("draft", "target") if role in r2) + "; decode %.0f tokens/s (native decoder stack), %.0f "
-              "(layers from Python)" % (r2["throughput"]["native_decoder_stack"]["decode_tokens_per_s"],
-                                         r2["throughput"]["python_layers"]["decode_tokens_per_s"]),
+            for role in ("draft", "target") if role in r2) + "; decode %.0f tokens/s (native decoder stack, "
+              "draft and target streams), %.0f (one stream), %.0f (layers from Python)"
+              % tuple(r2["throughput"][k]["decode_tokens_per_s"]
+                      for k in ("native_decoder_stack", "native_one_stream", "python_layers")),
               file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
     line = {

@@ -109,7 +109,7 @@ class RandomQwen3:
         self.cos, self.sin = model_rope_cache(mc, width * 16 + 1, dev)
         self.check = None  # (layer, callback) of a sampled attention check
         self.native = native
-        self.stack = None  # the native decoder stack, built on first use
+        self.stacks = {}  # native decoder stacks by lane (one per concurrent stream), built on first use
 
     def _token_tensor(self, tokens) -> torch.Tensor:
         """Token ids as a device int64 tensor (a device tensor passes through;
@@ -176,15 +176,17 @@ class RandomQwen3:
                                           st.max_prefill_len, softmax_scale=st.softmax_scale)
         return self._forward(st, [t for p in prompts for t in p], attention)
 
-    def decode(self, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False):
+    def decode(self, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False, lane: int = 0):
         """Decode / verify rows (rows of one sequence contiguous, seq_lens
         rising by one); returns the greedy next token of every row.  `tokens`
         is a host list or an int64 device tensor; with ``as_tensor`` the result
-        stays on the device (no host synchronisation)."""
+        stays on the device (no host synchronisation).  Forwards that may run
+        at the same time (other streams) take different ``lane`` numbers: each
+        lane has its own native stack buffers (the weights are shared)."""
         mc, dev = self.mc, self.dev
         st = build_infer_state(seq_ids, seq_lens, [], mc, self.cos, self.sin, dev)
         if self.native and len(tokens) <= DECODER_MAX_ROWS and not PHASE_RANGES:
-            return self._decode_native(st, seq_ids, seq_lens, tokens, as_tensor)
+            return self._decode_native(st, seq_ids, seq_lens, tokens, as_tensor, lane)
         hq = mc.num_q_heads
 
         def attention(li, lw, q_rows, k, v):
@@ -207,17 +209,18 @@ class RandomQwen3:
             return o
         return self._forward(st, tokens, attention, as_tensor)
 
-    def _decode_native(self, st, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False):
+    def _decode_native(self, st, seq_ids: list, seq_lens: list, tokens, as_tensor: bool = False, lane: int = 0):
         """decode() with every layer in one call of the native decoder stack;
         a sampled attention check receives its layer's q, o and LSE after
         the forward (later layers write only their own cache slots)."""
         mc, dev = self.mc, self.dev
-        if self.stack is None:
-            self.stack = DecoderStack(mc, self.layers)
+        stack = self.stacks.get(lane)
+        if stack is None:
+            stack = self.stacks[lane] = DecoderStack(mc, self.layers)
         x = self.embed[self._token_tensor(tokens)]
         res = torch.zeros_like(x)
         probe_layer = self.check[0] if self.check is not None else -1
-        probe = self.stack.forward(x, res, self.k_cache, self.v_cache, self.block_table, self.ec, st, self.cos,
+        probe = stack.forward(x, res, self.k_cache, self.v_cache, self.block_table, self.ec, st, self.cos,
                                    self.sin, probe_layer)
         if probe is not None:
             q, o, lse = probe
@@ -237,7 +240,7 @@ def _sync(dev: torch.device) -> None:
 def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_batch=64,
         target_batch=16, depth=4, seed=0, check_every=0, make_check=None, device="cuda:0",
         draft_cfg=QWEN3_0_6B, target_cfg=QWEN3_8B, share_weights=False, return_outputs=False,
-        log=None, native=True, sync_each_forward=False, overlap=True) -> dict:
+        log=None, native=True, sync_each_forward=False, overlap=True, target_streams=2) -> dict:
     """The speculative loop over `n_requests` synthetic requests; returns a summary.
 
     With ``check_every`` > 0, every check_every-th forward calls
@@ -262,7 +265,10 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     forwards on one stream and the target's on another, the target's waiting
     for its group's proposals by an event, and reads a group's results back
     after the next group is enqueued: the next group's draft forwards then
-    run beside this group's verifies.  Results are the same either way.
+    run beside this group's verifies.  A group's target batches alternate
+    over ``target_streams`` streams (each with its own decoder-stack lane),
+    so verifies of different batches run side by side too.  Results are the
+    same either way.
     """
     dev = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -304,7 +310,7 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
     # workers run side by side (streams at the default priority)
     overlap = overlap and not sync_each_forward and dev.type == "cuda"
     d_stream = torch.cuda.Stream(device=dev) if overlap else None
-    t_stream = torch.cuda.Stream(device=dev) if overlap else None
+    t_streams = [torch.cuda.Stream(device=dev) for _ in range(max(1, target_streams))] if overlap else [None]
 
     def on(stream):
         return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
@@ -361,14 +367,16 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
             drafted = torch.cuda.Event() if overlap else None
             if overlap:
                 drafted.record(d_stream)
-        with on(t_stream):
-            if overlap:
-                t_stream.wait_event(drafted)
-                # made on the draft stream, read on this one
-                props_dev.record_stream(t_stream)
-                rows_dev.record_stream(t_stream)
-            posts = []
-            for ts in range(0, len(dgroup), target_batch):
+        if overlap:
+            for ts_ in t_streams:
+                ts_.wait_event(drafted)
+                # made on the draft stream, read on the target streams
+                props_dev.record_stream(ts_)
+                rows_dev.record_stream(ts_)
+        posts_h = []
+        for b, ts in enumerate(range(0, len(dgroup), target_batch)):
+            lane = b % len(t_streams)
+            with on(t_streams[lane]):
                 tgroup = dgroup[ts:ts + target_batch]
                 sids, slens = [], []
                 for r in tgroup:
@@ -379,24 +387,28 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                     target.check = (target.mc.num_layers // 2, make_check())
                     n_checks += 1
                 step += 1
-                posts.append((tgroup, target.decode(sids, slens, rows_dev[ts:ts + len(tgroup)].reshape(-1),
-                                                    as_tensor=True)))
+                post = target.decode(sids, slens, rows_dev[ts:ts + len(tgroup)].reshape(-1), as_tensor=True,
+                                     lane=lane)
                 stats["target_forwards"] += 1
                 if sync_each_forward:
                     _sync(dev)
-            # one read-back per draft group: the proposals, then each batch's tokens
+                # one read-back per draft group: the proposals, then each batch's tokens
+                posts_h.append((tgroup, to_host(post)))
+        with on(t_streams[0]):
             props_h = to_host(props_dev)
-            posts_h = [(tgroup, to_host(post)) for tgroup, post in posts]
-            done = torch.cuda.Event() if dev.type == "cuda" else None
-            if done is not None:
-                done.record()
+        done = []
+        if dev.type == "cuda":
+            for ts_ in t_streams:
+                ev = torch.cuda.Event()
+                ev.record(ts_ if ts_ is not None else torch.cuda.current_stream(dev))
+                done.append(ev)
         return dgroup, props_h, posts_h, done
 
     def finish_group(pending) -> None:
         """Greedy acceptance of a group whose verifies were enqueued."""
         dgroup, props_h, posts_h, done = pending
-        if done is not None:
-            done.synchronize()
+        for ev in done:
+            ev.synchronize()
         props_host = props_h.tolist()
         props = {r: props_host[i] for i, r in enumerate(dgroup)}
         for tgroup, post_h in posts_h:
@@ -459,10 +471,13 @@ def main():
                    help="run decode/verify layers from Python instead of the native decoder stack")
     p.add_argument("--no-overlap", action="store_true",
                    help="draft and target forwards on one stream (no draft/verify overlap)")
+    p.add_argument("--target-streams", type=int, default=2,
+                   help="streams a draft group's target batches alternate over")
     a = p.parse_args()
     res = run(a.requests, a.prompt_lo, a.prompt_hi, a.new_tokens, a.draft_batch, a.target_batch,
               a.depth, a.seed, share_weights=a.share_weights, log=lambda m: print(m, flush=True),
-              native=not a.python_layers, overlap=not a.no_overlap)
+              native=not a.python_layers, overlap=not a.no_overlap,
+              target_streams=a.target_streams)
     print(json.dumps(res), flush=True)
 
 

@@ -74,8 +74,8 @@ def test_speculative_loop_shared_weights_accepts(gpu):
 def test_speculative_loop_pipelined_equals_synchronous(gpu):
     """Forwards enqueued back to back with device-resident proposals, with
     the draft and target on two streams (two draft groups per round, so a
-    group's draft forwards run beside the previous group's verifies) and on
-    one, give the same tokens and counters as waiting for every forward
+    group's draft forwards run beside the previous group's verifies), a
+    group's target batches on two streams or one, and all on one stream, give the same tokens and counters as waiting for every forward
     (deterministic kernels), with proposals accepted and two-row reconcile
     groups present."""
     kw = dict(n_requests=24, prompt_lo=64, prompt_hi=400, new_tokens=12, draft_batch=16, target_batch=8,
@@ -83,12 +83,13 @@ def test_speculative_loop_pipelined_equals_synchronous(gpu):
     a = run(**kw)
     b = run(**kw, sync_each_forward=True)
     c = run(**kw, overlap=False)
+    d = run(**kw, target_streams=1)
     print({k: v for k, v in a.items() if k != "outputs"}, flush=True)
     assert a["reconcile_groups"] > 0 and a["accepted"] > 0
-    assert a["outputs"] == b["outputs"] == c["outputs"]
+    assert a["outputs"] == b["outputs"] == c["outputs"] == d["outputs"]
     for key in ("accepted", "proposed", "reconcile_groups", "full_accepts", "partial_accepts", "rounds",
                 "target_forwards", "draft_forwards"):
-        assert a[key] == b[key] == c[key], key
+        assert a[key] == b[key] == c[key] == d[key], key
 
 
 def test_prefill_ignore_kvcache_leaves_cache(gpu):

@@ -64,7 +64,7 @@ class ScriptedModel:
             out.append(self._token(self.cache[r]))
         return out
 
-    def decode(self, seq_ids, seq_lens, tokens, as_tensor=False):
+    def decode(self, seq_ids, seq_lens, tokens, as_tensor=False, lane=0):
         if isinstance(tokens, torch.Tensor):  # the loop passes device-resident proposals
             tokens = tokens.tolist()
         assert len(seq_ids) == len(seq_lens) == len(tokens)
