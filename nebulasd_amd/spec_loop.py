@@ -427,18 +427,31 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
                     draft_missing[r] = props[r][-1]
                 out[r] += acc
 
+    early = None  # the next round's first group, enqueued before this round's last read-back
     while True:
         live = [r for r in range(n_requests) if len(out[r]) < new_tokens]
         if not live:
             break
         stats["rounds"] += 1
+        groups = [live[ds:ds + draft_batch] for ds in range(0, len(live), draft_batch)]
         # group g's acceptance is read back after group g + 1 is enqueued
         pending = None
-        for ds in range(0, len(live), draft_batch):
-            nxt_pending = enqueue_group(live[ds:ds + draft_batch])
+        for gi, dgroup in enumerate(groups):
+            if gi == 0 and early is not None:
+                if early[0] != dgroup:
+                    raise RuntimeError("the round's first draft group changed after it was enqueued")
+                nxt_pending, early = early, None
+            else:
+                nxt_pending = enqueue_group(dgroup)
             if pending is not None:
                 finish_group(pending)
             pending = nxt_pending
+        # The first group's requests are the lowest live ones: if none of
+        # them has finished they open the next round too, and their results
+        # are in, so their next proposals go out before the last group's
+        # read-back (other requests: the same work in the same order).
+        if len(groups) > 1 and all(len(out[r]) < new_tokens for r in groups[0]):
+            early = enqueue_group(groups[0])
         finish_group(pending)
         if log:
             log(f"round {stats['rounds']}: {sum(min(len(o), new_tokens) for o in out)} tokens")
