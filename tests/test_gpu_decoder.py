@@ -63,7 +63,7 @@ def test_decoder_stack_equals_python_layers(gpu, cfg, n_layers, n_req, depth):
     out_a = a.decode(sids, slens, toks)
     out_b = b.decode(sids, slens, toks)
     torch.cuda.synchronize()
-    assert a.stack is not None and b.stack is None, "expected one native and one Python forward"
+    assert a.stacks and not b.stacks, "expected one native and one Python forward"
     for x, y, what in ((a.k_cache, b.k_cache, "k_cache"), (a.v_cache, b.v_cache, "v_cache")):
         err = (x.float() - y.float()).abs().max().item()
         print(f"  {what}: max |native - python| = {err:.2e}", flush=True)
