@@ -304,9 +304,9 @@ def run(n_requests=512, prompt_lo=128, prompt_hi=1024, new_tokens=128, draft_bat
              "accepted": 0, "reconcile_groups": 0, "full_accepts": 0, "partial_accepts": 0,
              "multi_token_appends": 0}
     step = 0
-    # draft forwards on one stream, target verifies on another: a draft
-    # group's forwards run beside the previous group's verifies (other
-    # requests, the other model), as the reference's draft and target
+    # draft forwards on one stream, target verifies on `target_streams` more:
+    # a draft group's forwards run beside the previous group's verifies
+    # (other requests, the other model), as the reference's draft and target
     # workers run side by side (streams at the default priority)
     overlap = overlap and not sync_each_forward and dev.type == "cuda"
     d_stream = torch.cuda.Stream(device=dev) if overlap else None
