@@ -1254,6 +1254,102 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+# The stdout line is read back from a bounded tail of the run's output: it
+# keeps the headline, the roofline, the CPU baseline, the probes and a few
+# scalar figures per secondary leg, and stays under this many bytes.  The
+# full per-leg results go to stderr as one "# detail " JSON line.
+LINE_MAX_BYTES = 7500
+# Scalar figures a secondary leg keeps on the stdout line, when it has them.
+LEG_KEYS = ("us_per_layer_call", "hbm_gbps", "hbm_frac", "frac_of_gather_floor", "tflops", "mfma_frac",
+            "us_per_write", "reference_us_per_write", "us_per_layer", "floor_us_at_copy_rate",
+            "reference_sdpa_loop_us", "us_per_call", "reference_us_per_call", "us_per_call_graph")
+# Second-level dicts of a leg whose scalar figures are kept as well.
+LEG_SUBKEYS = ("kv_gather_floor", "native_decoder_stack", "throughput", "draft", "target", "D2H", "H2D")
+
+
+def _sig(x):
+    """x rounded to 5 significant digits (ints and non-numbers unchanged)."""
+    if isinstance(x, bool) or not isinstance(x, float):
+        return x
+    return float(f"{x:.5g}")
+
+
+def _compact_cpu(c):
+    if not isinstance(c, dict):
+        return None
+    return {k: _sig(c[k]) for k in ("value", "unit", "cores", "kind") if k in c}
+
+
+def _scalars(d: dict, keys) -> dict:
+    return {k: _sig(d[k]) for k in keys if isinstance(d.get(k), (int, float)) and not isinstance(d.get(k), bool)}
+
+
+def compact_leg(r: dict) -> dict:
+    """The figures of one secondary leg that the stdout line keeps."""
+    out = _scalars(r, LEG_KEYS)
+    for sub in LEG_SUBKEYS:
+        v = r.get(sub)
+        if not isinstance(v, dict):
+            continue
+        s = _scalars(v, LEG_KEYS + ("decode_tokens_per_s", "us_per_layer_call_median", "gbps", "kernel_gbps",
+                                    "dma_gbps", "reference_gbps"))
+        for k2, v2 in v.items():  # one more level (e.g. throughput variants, per-shape layers)
+            if isinstance(v2, dict):
+                s2 = _scalars(v2, ("decode_tokens_per_s", "us_per_layer", "us_per_call"))
+                if s2:
+                    s[k2] = s2
+        if s:
+            out[sub] = s
+    for k, v in r.items():  # rest-of-layer legs: one dict per kernel and shape
+        if k not in LEG_SUBKEYS and isinstance(v, dict) and "us_per_call" in v:
+            out[k] = _scalars(v, ("us_per_call", "reference_us_per_call", "us_per_call_graph",
+                                  "library_us_per_call_graph", "gbps"))
+    cpu = _compact_cpu(r.get("cpu_baseline"))
+    if cpu:
+        out["cpu_baseline"] = cpu
+    return out
+
+
+PROBE_KEYS = ("gbps", "frac_of_peak", "us", "us_per_launch", "us_per_layer_call", "best_gbps", "workgroups",
+              "grid", "unroll", "ring", "per_cu")
+
+
+def _compact_probes(probes: dict) -> dict:
+    """Probe figures for the stdout line: the scalars of each probe and of
+    its best sweep point (sweeps themselves stay in the detail line)."""
+    out = {}
+    for name, p in probes.items():
+        if not isinstance(p, dict):
+            out[name] = _sig(p)
+            continue
+        s = _scalars(p, PROBE_KEYS)
+        for k, v in p.items():
+            if isinstance(v, dict) and k.startswith("best"):
+                s[k] = _scalars(v, PROBE_KEYS)
+        out[name] = s
+    return out
+
+
+def stdout_line(line: dict, secondary: dict) -> str:
+    """The JSON line for stdout: `line` plus the compact secondary legs,
+    dropping leg detail (then whole legs, last first) until it fits in
+    LINE_MAX_BYTES."""
+    legs = {name: compact_leg(r) for name, r in secondary.items()}
+    out = dict(line, secondary=legs)
+    text = json.dumps(out)
+    if len(text.encode()) <= LINE_MAX_BYTES:
+        return text
+    for name in legs:  # keep only the top-level scalars and the CPU baseline
+        legs[name] = {k: v for k, v in legs[name].items() if not isinstance(v, dict) or k == "cpu_baseline"}
+    text = json.dumps(out)
+    for name in reversed(list(legs)):
+        if len(text.encode()) <= LINE_MAX_BYTES:
+            break
+        del legs[name]
+        text = json.dumps(out)
+    return text
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -1402,12 +1498,13 @@ def main():
             "kernels": "paged_attn_kernel (+ combine_kernel for split segments), one layer call",
         },
         "copy_probe_gbps": copy_gbps,
-        "probes": probes,
+        "probes": _compact_probes(probes),
         "cpu_baseline": cpu,
-        "detail": res,
-        "secondary": secondary,
+        "detail": compact_leg(res),
     }
-    print(json.dumps(line), flush=True)
+    print("# detail " + json.dumps({"detail": res, "probes": probes, "secondary": secondary}),
+          file=sys.stderr, flush=True)
+    print(stdout_line(line, secondary), flush=True)
 
 
 if __name__ == "__main__":
