@@ -37,6 +37,52 @@ int nsd_probe_tile_gather(const void* k_cache, const void* v_cache, int64_t cach
                           const int64_t* tiles, int64_t n_tiles, const int64_t* worker_start,
                           int n_workers, uint32_t* sink, void* stream);
 
+/*
+ * nsd_probe_stream_read_unroll: as nsd_probe_stream_read (which uses unroll
+ * 4), with `unroll` (1, 2, 4, 8 or 16) 16-byte loads in flight per thread
+ * and chunk; `bytes` a positive multiple of 64 KiB.
+ */
+int nsd_probe_stream_read_unroll(const void* src, int64_t bytes, uint32_t* sink, int grid, int unroll,
+                                 void* stream);
+
+/*
+ * nsd_probe_gather_pieces: the tiles of nsd_probe_tile_gather cut into
+ * `n_pieces` pieces; workgroup p streams tiles [piece_start[p],
+ * piece_start[p + 1]) (at most 256) through an LDS ring of `ring` (3, 4, 6,
+ * 8, 12 or 16) K+V items, as the hardware dispatches it.  Each workgroup
+ * takes ring * 8 KiB + 2 KiB + lds_extra bytes of LDS (at most 160 KiB), which
+ * sets how many share a CU.
+ */
+int nsd_probe_gather_pieces(const void* k_cache, const void* v_cache, int64_t cache_elems,
+                            const int64_t* tiles, int64_t n_tiles, const int64_t* piece_start,
+                            int n_pieces, int ring, int lds_extra, uint32_t* sink, void* stream);
+
+/*
+ * nsd_probe_gather_vgpr: the pieces of nsd_probe_gather_pieces read into
+ * registers, `unroll` (1, 2 or 4) K+V tiles per wave and round.
+ */
+int nsd_probe_gather_vgpr(const void* k_cache, const void* v_cache, int64_t cache_elems,
+                          const int64_t* tiles, int64_t n_tiles, const int64_t* piece_start,
+                          int n_pieces, int unroll, uint32_t* sink, void* stream);
+
+/*
+ * nsd_probe_gather_wave: the pieces of nsd_probe_gather_pieces streamed by
+ * each wave on its own (wave w takes tiles w, w + 4, ... of its workgroup's
+ * piece; no barriers), `round_tiles` (1 or 2) tiles per round with the next
+ * round in flight.  k_mode 1 reads K in the A-operand layout of
+ * v_mfma_f32_16x16x32_f16 (16 rows x 64 B per load), 0 in contiguous 1 KB
+ * runs; v_mode 0 reads V into registers, 1 into the wave's own LDS slots by
+ * global_load_lds_dwordx4.  LDS: 2 KiB + (v_mode ? 64 KiB * round_tiles : 0)
+ * + lds_extra bytes per workgroup.
+ */
+int nsd_probe_gather_wave(const void* k_cache, const void* v_cache, int64_t cache_elems,
+                          const int64_t* tiles, int64_t n_tiles, const int64_t* piece_start,
+                          int n_pieces, int round_tiles, int k_mode, int v_mode, int lds_extra,
+                          uint32_t* sink, void* stream);
+
+/* nsd_probe_empty: launch a kernel of `grid` one-wave workgroups that does nothing. */
+int nsd_probe_empty(int grid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

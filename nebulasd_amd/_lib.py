@@ -27,8 +27,8 @@ COPY_ENGINE_KERNEL = 1
 
 # Plan header word indices (nsd_common.h, enum PlanHeader).
 PLAN_MAGIC, PLAN_VERSION, PLAN_ROWS, PLAN_GROUPS, PLAN_PIECES, PLAN_WORKERS, PLAN_COMBINES, \
-    PLAN_SLOTS, PLAN_ROWS_MAX, PLAN_HQ, PLAN_HKV, PLAN_OFF_GROUPS, PLAN_OFF_WSTART, \
-    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_STRIDE, PLAN_BT_ROWS, \
+    PLAN_SLOTS, PLAN_ROWS_MAX, PLAN_HQ, PLAN_HKV, PLAN_OFF_GROUPS, PLAN_SIZED_FOR, \
+    PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_BLOCKS, PLAN_BT_ROWS, \
     PLAN_BT_STRIDE, PLAN_MAX_BLOCKS = range(20)
 
 _I32P = POINTER(c_int32)
@@ -110,6 +110,16 @@ SIGNATURES = {
     "nsd_probe_stream_read": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
     "nsd_probe_tile_gather": (
         c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p, c_void_p]),
+    "nsd_probe_stream_read_unroll": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p]),
+    "nsd_probe_gather_pieces": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_void_p,
+                c_void_p]),
+    "nsd_probe_gather_vgpr": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "nsd_probe_empty": (c_int, [c_int, c_void_p]),
+    "nsd_probe_gather_wave": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                c_void_p, c_void_p]),
     "nsd_prefill_attention": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                 c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),

@@ -22,62 +22,57 @@ int up_gate_silu_gated(const void* x, const void* up_gate, void* y, int64_t n_ro
 // Plan word layout (int32), shared by the planner and the attention launch.
 enum PlanHeader {
   kPlanMagic = 0,      // 0x4E534450
-  kPlanVersion,        // 2
+  kPlanVersion,        // kPlanVersionValue
   kPlanRows,           // decode/verify rows covered
   kPlanGroups,         // verify groups
-  kPlanPieces,         // (segment, block range) pieces
-  kPlanWorkers,        // launch grid (multiple of 8)
+  kPlanPieces,         // piece records (one workgroup each; empty records pad the XCD lists)
+  kPlanWorkers,        // launch grid: equal to kPlanPieces, a multiple of 8
   kPlanCombines,       // segments cut into >1 piece
   kPlanSlots,          // partial slots
   kPlanRowsMax,        // max query rows per (group, kv head)
   kPlanHq,
   kPlanHkv,
   kPlanOffGroups,      // word offset of groups [n_groups][4] {row_start, q_len, seq_id, ctx}
-  kPlanOffWorkers,     // word offset of the worker table [n_workers][kWorkerWords]
+  kPlanSizedFor,       // the n_workers (wave slots) the piece size was chosen for
   kPlanOffPieces,      // word offset of pieces [n_pieces][kPieceWords]
   kPlanOffCombines,    // word offset of combines [n_combines][kPieceWords]
   kPlanWords,          // total words
-  kPlanPieceStride,    // piece records per worker: worker w's records start at w * stride
+  kPlanPieceBlocks,    // target blocks per piece
   kPlanBtRows,         // block-table rows every piece's seq_id was checked against
   kPlanBtStride,       // block-table row length every piece's block range was checked against
-  kPlanMaxBlocks,      // most 16-token blocks one worker streams
+  kPlanMaxBlocks,      // most 16-token blocks in one piece
 };
 static_assert(kPlanMaxBlocks < NSD_PLAN_HEADER_WORDS, "plan header size");
 
 // A piece: blocks [blk_begin, blk_end) of one (group, kv head) segment, with
-// the group's description inlined so a worker needs one record per piece.
-// kPieceKvBase counts the blocks of the worker's earlier pieces: the piece's
-// block ids sit at that offset of the worker's id list.
+// the group's description inlined so a workgroup needs one record.  A record
+// with q_len 0 is empty (it pads an XCD's list; its workgroup exits at once).
 enum PieceField {
   kPieceHead = 0,   // kv head
   kPieceBlkBegin,   // first 16-token block
   kPieceBlkEnd,     // one past the last block
   kPieceSlot,       // partial slot, or -1 when the piece is the whole segment
   kPieceRowStart,   // first decode row of the group
-  kPieceQLen,       // rows in the group
+  kPieceQLen,       // rows in the group (0: empty record)
   kPieceSeqId,      // block-table row
   kPieceCtx,        // tokens before the group's first new token
   kPieceComb,       // combine record of the segment, or -1
   kPieceCombFirst,  // first partial slot of the segment
   kPieceCombSlots,  // partial slots of the segment
-  kPieceKvBase,     // blocks of this worker's pieces before this one
+  kPieceSeg,        // segment index (group * Hkv + kv head)
   kPieceWords,
 };
-// A worker-table row: {first piece, end piece, <first piece record>, 0, 0}.
-// Worker w's records are pieces [w * stride, w * stride + count), so the
-// kernel loads them without reading the table first.
-constexpr int kWorkerWords = 16;
-constexpr int kWorkerFirstPiece = 2;
 // A combine record: {kv head, first slot, slot count, row start, q_len, 0, 0, 0}.
 enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
 
 constexpr int32_t kPlanMagicValue = 0x4E534450;
-constexpr int32_t kPlanVersionValue = 7;
+constexpr int32_t kPlanVersionValue = 8;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
-constexpr int kMaxGroupRows = 64;
+constexpr int kMaxGroupRows = 48;       // query rows of one segment: three 16-row tiles in one wave
 constexpr int kMaxSlotsPerSegment = 128;
-constexpr int kMaxWorkerPieces = 4;    // pieces one workgroup streams (their query rows stay in registers)
-constexpr int kMaxWorkerBlocks = 1024; // blocks one workgroup streams (its LDS id list)
+constexpr int kMaxPieceBlocks = 256;    // blocks of one piece (four waves, one block id per lane)
+constexpr int kMinPieceBlocks = 4;
+constexpr int kXcds = 8;                // workgroup i of a launch runs on XCD i % 8
 
 }  // namespace nsd

@@ -13,21 +13,6 @@ namespace nsd {
 
 namespace {
 thread_local std::string g_last_error;
-// Cost model of the planner, in 16-token blocks of streaming: a piece costs
-// its blocks plus a fixed kPieceCostBlocks for what it adds to the stream
-// (the ring items that bring its query rows, the output or partial it
-// writes).  A worker opens another piece only if at least kMinPieceBlocks of
-// its budget remain for it.
-constexpr int64_t kMinPieceBlocks = 4;
-constexpr int64_t kPieceCostBlocks = 3;
-// Workgroups launch in index order, two per CU: the first half of the grid
-// takes one slot on every CU before the second half arrives, and a CU's
-// earlier workgroup streams a few percent faster than its later one
-// (per-workgroup timelines).  The first half's ranges are cut 1.5% longer,
-// the second half's 1.5% shorter (per mille of the cost cap); the plan stays
-// a function of the forward's rows alone.
-constexpr int64_t kFirstHalfPerMille = 1015;
-constexpr int64_t kSecondHalfPerMille = 985;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -53,11 +38,11 @@ static int64_t round_up8(int64_t x) { return (x + 7) / 8 * 8; }
 extern "C" int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_workers) {
   if (n_rows < 0 || num_kv_heads <= 0 || n_workers <= 0) return -1;
   const int64_t segs = n_rows * num_kv_heads;
-  const int64_t nw = round_up8(n_workers);
-  // piece records: at most min(32, pieces) per worker, at a fixed stride
-  const int64_t stride = std::min<int64_t>(kMaxWorkerPieces, nw + segs);
-  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kWorkerWords * nw + kPieceWords * nw * stride +
-         kPieceWords * segs;
+  // pieces: at most n_workers + segs for the chosen piece size (each segment
+  // adds at most one short piece), plus the empty records that even out the
+  // XCD lists; a plan that needs more reports its size and the caller retries
+  const int64_t pieces = round_up8((int64_t)n_workers + segs) + kXcds * kMaxSlotsPerSegment;
+  return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kPieceWords * pieces + kPieceWords * segs;
 }
 
 extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
@@ -118,134 +103,101 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   }
   const int64_t total = seg_start[n_segs];
 
-  // 3. contiguous block ranges per worker of near-equal cost (the cost model
-  //    above, weighted by dispatch half).  The target cost is the smallest one that fits the stream into
-  //    the workers; it also keeps every segment under kMaxSlotsPerSegment
-  //    pieces, every worker under kMaxWorkerPieces pieces and
-  //    kMaxWorkerBlocks blocks.
+  // 3. pieces: every segment is cut into near-equal pieces of about
+  //    `target` blocks, where target spreads the stream over the n_workers
+  //    wave slots (at least kMinPieceBlocks, at most kMaxPieceBlocks, and
+  //    few enough pieces per segment for kMaxSlotsPerSegment partials).
   int64_t max_seg = 0;
   for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
-  const int64_t cmin = kPieceCostBlocks + std::max<int64_t>(
-      kMinPieceBlocks, (max_seg + kMaxSlotsPerSegment - 3) / (kMaxSlotsPerSegment - 2));
-  // Greedy cut of the stream for a per-worker cost cap; returns the workers used
-  // and, if `cuts` is given, each worker's piece boundaries.
-  const int64_t first_half = std::max<int64_t>(1, n_workers) / 2;
-  auto cut_stream = [&](int64_t cap, std::vector<int64_t>* cuts) {
-    int64_t used = 0, pos = 0, seg_i = 0;
-    while (pos < total) {
-      int64_t budget = cap * (used < first_half ? kFirstHalfPerMille : kSecondHalfPerMille) / 1000;
-      int64_t room = kMaxWorkerBlocks;
-      int opened = 0;
-      if (cuts) cuts->push_back(-1);  // worker marker
-      while (pos < total && opened < kMaxWorkerPieces && room > 0) {
-        while (seg_start[seg_i + 1] <= pos) ++seg_i;
-        if (opened > 0 && budget < kPieceCostBlocks + kMinPieceBlocks) break;
-        const int64_t take = std::min(room, std::max<int64_t>(
-            1, std::min(budget - kPieceCostBlocks, seg_start[seg_i + 1] - pos)));
-        if (cuts) cuts->insert(cuts->end(), {pos, pos + take});
-        pos += take;
-        room -= take;
-        budget -= kPieceCostBlocks + take;
-        ++opened;
-        if (budget <= 0) break;
-      }
-      ++used;
-    }
-    return used;
-  };
-  const int64_t want = std::max<int64_t>(1, n_workers);
-  int64_t lo = cmin, hi = std::max(cmin, total + n_segs * (kPieceCostBlocks + 1));
-  if (total > 0 && cut_stream(lo, nullptr) > want) {
-    while (lo + 1 < hi) {  // smallest cap that fits in `want` workers
-      const int64_t mid = (lo + hi) / 2;
-      if (cut_stream(mid, nullptr) <= want) hi = mid; else lo = mid;
-    }
-    lo = hi;
+  int64_t target = total > 0 ? (total + n_workers - 1) / n_workers : kMinPieceBlocks;
+  target = std::max<int64_t>(target, kMinPieceBlocks);
+  target = std::max<int64_t>(target, (max_seg + kMaxSlotsPerSegment - 1) / kMaxSlotsPerSegment);
+  target = std::min<int64_t>(target, kMaxPieceBlocks);
+  if ((max_seg + target - 1) / target > kMaxSlotsPerSegment)
+    return fail(NSD_ERR_UNSUPPORTED, "plan: a segment of %lld blocks needs more than %d pieces of %d",
+                (long long)max_seg, kMaxSlotsPerSegment, kMaxPieceBlocks);
+  std::vector<int64_t> seg_pieces(n_segs);
+  for (int64_t s = 0; s < n_segs; ++s) {
+    const int64_t nb = seg_start[s + 1] - seg_start[s];
+    seg_pieces[s] = (nb + target - 1) / target;
   }
-  std::vector<int64_t> cuts;
-  const int64_t active = total > 0 ? cut_stream(lo, &cuts) : 0;
-  const int64_t grid = total > 0 ? round_up8(active) : 0;
-  std::vector<int32_t> wstart(grid + 1, 0);
-  std::vector<int32_t> pieces;  // kPieceWords per piece, workers' pieces in order
-  int64_t seg = 0, w = -1;
-  for (size_t c = 0; c < cuts.size();) {
-    if (cuts[c] < 0) {  // next worker
-      wstart[++w] = (int32_t)(pieces.size() / kPieceWords);
-      ++c;
-      continue;
-    }
-    const int64_t a = cuts[c], b = cuts[c + 1];
-    c += 2;
-    while (seg_start[seg + 1] <= a) ++seg;
-    const int32_t* g = &groups[4 * (seg / num_kv_heads)];
-    pieces.insert(pieces.end(), {(int32_t)(seg % num_kv_heads), (int32_t)(a - seg_start[seg]),
-                                 (int32_t)(b - seg_start[seg]), -1, g[0], g[1], g[2], g[3],
-                                 -1, 0, 0, 0});
-  }
-  for (int64_t v = w + 1; v < grid; ++v) wstart[v] = (int32_t)(pieces.size() / kPieceWords);
-  wstart[grid] = (int32_t)(pieces.size() / kPieceWords);
-  const int64_t n_pieces = (int64_t)pieces.size() / kPieceWords;
 
-  // 4. partial slots for segments cut into several pieces (pieces of one
-  //    segment are adjacent because workers walk the block stream in order).
-  std::vector<int32_t> combines;  // kPieceWords per record
-  int64_t n_slots = 0;
-  auto same_seg = [&](int64_t i, int64_t j) {
-    const int32_t* x = &pieces[kPieceWords * i];
-    const int32_t* y = &pieces[kPieceWords * j];
-    return x[kPieceHead] == y[kPieceHead] && x[kPieceRowStart] == y[kPieceRowStart];
+  // 4. segments to XCDs (workgroup i runs on XCD i % 8): longest first, each
+  //    to the XCD with the fewest blocks so far, so a segment's pieces share
+  //    one L2 (its query rows) and every XCD gets near-equal work.  Each
+  //    XCD's pieces then go longest first, so the shortest come last.
+  std::vector<int64_t> order(n_segs);
+  for (int64_t s = 0; s < n_segs; ++s) order[s] = s;
+  std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) {
+    return seg_start[x + 1] - seg_start[x] > seg_start[y + 1] - seg_start[y];
+  });
+  std::vector<std::vector<std::pair<int64_t, int64_t>>> lists(kXcds);  // (segment, piece index)
+  std::vector<int64_t> load(kXcds, 0);
+  for (int64_t s : order) {
+    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    load[x] += seg_start[s + 1] - seg_start[s];
+    for (int64_t k = 0; k < seg_pieces[s]; ++k) lists[x].push_back({s, k});
+  }
+  auto piece_blocks = [&](int64_t s, int64_t k) {
+    const int64_t nb = seg_start[s + 1] - seg_start[s], n = seg_pieces[s];
+    return std::make_pair(k * nb / n, (k + 1) * nb / n);
   };
-  for (int64_t i = 0; i < n_pieces;) {
-    int64_t j = i + 1;
-    while (j < n_pieces && same_seg(i, j)) ++j;
-    if (j - i > kMaxSlotsPerSegment)
-      return fail(NSD_ERR_INVALID, "plan: segment cut into %lld pieces", (long long)(j - i));
-    if (j - i > 1) {
-      const int32_t* x = &pieces[kPieceWords * i];
-      const int32_t ci = (int32_t)(combines.size() / kPieceWords);
-      combines.insert(combines.end(), {x[kPieceHead], (int32_t)n_slots, (int32_t)(j - i),
-                                       x[kPieceRowStart], x[kPieceQLen], 0, 0, 0, 0, 0, 0, 0});
-      for (int64_t k = i; k < j; ++k) {
-        int32_t* y = &pieces[kPieceWords * k];
-        y[kPieceSlot] = (int32_t)(n_slots + (k - i));
-        y[kPieceComb] = ci;
-        y[kPieceCombFirst] = (int32_t)n_slots;
-        y[kPieceCombSlots] = (int32_t)(j - i);
-      }
-      n_slots += j - i;
-    }
-    i = j;
+  size_t longest = 0;
+  for (auto& l : lists) {
+    std::stable_sort(l.begin(), l.end(), [&](const std::pair<int64_t, int64_t>& x,
+                                            const std::pair<int64_t, int64_t>& y) {
+      const auto bx = piece_blocks(x.first, x.second), by = piece_blocks(y.first, y.second);
+      return bx.second - bx.first > by.second - by.first;
+    });
+    longest = std::max(longest, l.size());
+  }
+
+  // 5. partial slots for segments cut into several pieces, in segment order.
+  std::vector<int32_t> combines;  // kPieceWords per record
+  std::vector<int64_t> seg_slot(n_segs, -1), seg_comb(n_segs, -1);
+  int64_t n_slots = 0;
+  for (int64_t s = 0; s < n_segs; ++s) {
+    if (seg_pieces[s] < 2) continue;
+    const int32_t* g = &groups[4 * (s / num_kv_heads)];
+    seg_comb[s] = (int64_t)combines.size() / kPieceWords;
+    seg_slot[s] = n_slots;
+    combines.insert(combines.end(), {(int32_t)(s % num_kv_heads), (int32_t)n_slots, (int32_t)seg_pieces[s],
+                                     g[0], g[1], 0, 0, 0, 0, 0, 0, 0});
+    n_slots += seg_pieces[s];
   }
   const int64_t n_combines = (int64_t)combines.size() / kPieceWords;
 
-  // 5. records at a fixed stride per worker (zero records fill the gaps),
-  //    each with the blocks of its worker's earlier pieces; the worker table
-  //    holds each worker's record range and an inline copy of its first record.
-  int64_t stride = 0, max_blocks = 0;
-  for (int64_t v = 0; v < grid; ++v) stride = std::max<int64_t>(stride, wstart[v + 1] - wstart[v]);
-  std::vector<int32_t> records(kPieceWords * grid * stride, 0);
-  std::vector<int32_t> wtable(kWorkerWords * grid, 0);
-  for (int64_t v = 0; v < grid; ++v) {
-    int64_t blocks_run = 0;
-    for (int64_t i = wstart[v]; i < wstart[v + 1]; ++i) {
-      int32_t* r = &records[kPieceWords * (v * stride + (i - wstart[v]))];
-      std::copy(&pieces[kPieceWords * i], &pieces[kPieceWords * (i + 1)], r);
-      r[kPieceKvBase] = (int32_t)blocks_run;
-      blocks_run += r[kPieceBlkEnd] - r[kPieceBlkBegin];
+  // 6. records in dispatch order: position 8j + x holds the j-th piece of
+  //    XCD x's list, or an empty record where that list is shorter.
+  const int64_t grid = total > 0 ? kXcds * (int64_t)longest : 0;
+  std::vector<int32_t> records(kPieceWords * grid, 0);
+  int64_t max_blocks = 0;
+  for (int64_t j = 0; j < (int64_t)longest; ++j) {
+    for (int x = 0; x < kXcds; ++x) {
+      int32_t* r = &records[kPieceWords * (kXcds * j + x)];
+      if (j >= (int64_t)lists[x].size()) {
+        r[kPieceSlot] = -1;
+        r[kPieceComb] = -1;
+        r[kPieceSeg] = -1;
+        continue;
+      }
+      const int64_t s = lists[x][j].first, k = lists[x][j].second;
+      const auto b = piece_blocks(s, k);
+      const int32_t* g = &groups[4 * (s / num_kv_heads)];
+      const bool split = seg_pieces[s] > 1;
+      const int32_t rec[kPieceWords] = {
+          (int32_t)(s % num_kv_heads), (int32_t)b.first, (int32_t)b.second,
+          split ? (int32_t)(seg_slot[s] + k) : -1, g[0], g[1], g[2], g[3],
+          split ? (int32_t)seg_comb[s] : -1, split ? (int32_t)seg_slot[s] : 0,
+          split ? (int32_t)seg_pieces[s] : 0, (int32_t)s};
+      std::copy(rec, rec + kPieceWords, r);
+      max_blocks = std::max(max_blocks, b.second - b.first);
     }
-    max_blocks = std::max(max_blocks, blocks_run);
-    int32_t* row = &wtable[kWorkerWords * v];
-    row[0] = (int32_t)(v * stride);
-    row[1] = (int32_t)(v * stride + wstart[v + 1] - wstart[v]);
-    if (wstart[v] < wstart[v + 1])
-      std::copy(&records[kPieceWords * v * stride], &records[kPieceWords * (v * stride + 1)],
-                row + kWorkerFirstPiece);
   }
-  const int64_t n_records = grid * stride;
+  const int64_t n_records = grid;
 
   const int64_t off_groups = NSD_PLAN_HEADER_WORDS;
-  const int64_t off_wstart = off_groups + 4 * n_groups;
-  const int64_t off_pieces = off_wstart + kWorkerWords * grid;
+  const int64_t off_pieces = off_groups + 4 * n_groups;
   const int64_t off_combines = off_pieces + kPieceWords * n_records;
   const int64_t words = off_combines + kPieceWords * n_combines;
   if (words > plan_capacity) {
@@ -270,16 +222,15 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   h[kPlanHq] = num_q_heads;
   h[kPlanHkv] = num_kv_heads;
   h[kPlanOffGroups] = (int32_t)off_groups;
-  h[kPlanOffWorkers] = (int32_t)off_wstart;
+  h[kPlanSizedFor] = n_workers;
   h[kPlanOffPieces] = (int32_t)off_pieces;
   h[kPlanOffCombines] = (int32_t)off_combines;
   h[kPlanWords] = (int32_t)words;
-  h[kPlanPieceStride] = (int32_t)stride;
+  h[kPlanPieceBlocks] = (int32_t)target;
   h[kPlanBtRows] = (int32_t)std::min<int64_t>(bt_rows, INT32_MAX);
   h[kPlanBtStride] = (int32_t)std::min<int64_t>(bt_stride, INT32_MAX);
   h[kPlanMaxBlocks] = (int32_t)max_blocks;
   std::copy(groups.begin(), groups.end(), h + off_groups);
-  std::copy(wtable.begin(), wtable.end(), h + off_wstart);
   std::copy(records.begin(), records.end(), h + off_pieces);
   std::copy(combines.begin(), combines.end(), h + off_combines);
 

@@ -48,7 +48,7 @@ class LlamaInferState:
     # host copies of the decode rows (seq_ids[num_prefill_seqs:], decoding_seq_lens)
     seq_ids_list: list | None = None
     decoding_seq_lens_list: list | None = None
-    # verify grouping: 0 = pack up to 64 rows per (group, kv head); 1 = row-wise
+    # verify grouping: 0 = pack up to 48 rows per (group, kv head); 1 = row-wise
     max_group_rows: int = 0
     attn_plan: AttnPlan | None = None
 

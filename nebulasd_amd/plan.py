@@ -18,12 +18,15 @@ import numpy as np
 from . import _lib
 
 PIECE_WORDS = 12
-WORKER_WORDS = 16
+MAX_GROUP_ROWS = 48   # query rows of one (group, kv head): three 16-row tiles in one wave
+XCDS = 8              # workgroup i of a launch runs on XCD i % 8
 _workers_cache: dict[tuple[int, int], int] = {}
 
 
 def num_workers(max_rows: int, device_index: int | None = None) -> int:
-    """Workgroups that fill the current GPU for plans with ``max_rows`` rows per group."""
+    """Wave slots of the current GPU (CUs x attention workgroups per CU) for
+    plans with ``max_rows`` rows per group: the planner cuts the block
+    stream into about this many pieces."""
     import torch
 
     dev = torch.cuda.current_device() if device_index is None else device_index
@@ -35,6 +38,21 @@ def num_workers(max_rows: int, device_index: int | None = None) -> int:
             _lib.call("nsd_attn_num_workers", 16 * nt, ctypes.byref(out))
         _workers_cache[key] = int(out.value)
     return _workers_cache[key]
+
+
+# Pieces the planner aims for per workgroup slot: more, shorter pieces even
+# out the end of a launch; fewer, longer ones write fewer partials and merge
+# fewer wave states.  Measured: two per slot for one 16-row tile (decode,
+# 520-byte partials), one for wider groups (5-10 KB partials).
+PIECES_PER_SLOT = {1: 2.0, 2: 1.0, 3: 1.0}
+
+
+def pieces_for(slots: int, max_rows: int) -> int:
+    """The n_workers the planner is given for a device with `slots`
+    workgroup slots, for groups of at most `max_rows` query rows."""
+    per = PIECES_PER_SLOT
+    f = per if isinstance(per, (int, float)) else per[min(3, (max_rows + 15) // 16)]
+    return max(1, int(round(slots * f)))
 
 
 def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
@@ -70,36 +88,32 @@ def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim:
 def decode_plan(words: np.ndarray) -> dict:
     """Split plan words into named numpy views (for inspection and tests).
 
-    Worker w's piece records sit at ``records[w * piece_stride :]`` (the
-    kernel reads them without the worker table); ``pieces`` lists the used
-    records in worker order and ``worker_start`` indexes it.
+    ``records`` holds one piece per workgroup in dispatch order (record i runs
+    on XCD i % 8; records with q_len 0 are empty); ``pieces`` lists the
+    non-empty ones in that order.
     """
     h = words[:_lib.PLAN_HEADER_WORDS]
     n_groups, n_records = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_PIECES])
-    n_workers, n_comb = int(h[_lib.PLAN_WORKERS]), int(h[_lib.PLAN_COMBINES])
-    og, ow = int(h[_lib.PLAN_OFF_GROUPS]), int(h[_lib.PLAN_OFF_WSTART])
-    op, oc = int(h[_lib.PLAN_OFF_PIECES]), int(h[_lib.PLAN_OFF_COMBINES])
-    table = words[ow:ow + WORKER_WORDS * n_workers].reshape(n_workers, WORKER_WORDS)
+    n_comb = int(h[_lib.PLAN_COMBINES])
+    og, op, oc = int(h[_lib.PLAN_OFF_GROUPS]), int(h[_lib.PLAN_OFF_PIECES]), int(h[_lib.PLAN_OFF_COMBINES])
     # {kv head, blk_begin, blk_end, slot, row_start, q_len, seq_id, ctx,
-    #  combine, combine first slot, combine slots, worker's blocks before it}
+    #  combine, combine first slot, combine slots, segment}
     records = words[op:op + PIECE_WORDS * n_records].reshape(n_records, PIECE_WORDS)
-    used = [i for w in range(n_workers) for i in range(int(table[w, 0]), int(table[w, 1]))]
-    counts = [int(table[w, 1] - table[w, 0]) for w in range(n_workers)]
+    used = records[:, 5] > 0
     return {
         "rows": int(h[_lib.PLAN_ROWS]),
-        "workers": n_workers,
+        "workers": int(h[_lib.PLAN_WORKERS]),
         "slots": int(h[_lib.PLAN_SLOTS]),
         "rows_max": int(h[_lib.PLAN_ROWS_MAX]),
-        "piece_stride": int(h[_lib.PLAN_PIECE_STRIDE]),
+        "sized_for": int(h[_lib.PLAN_SIZED_FOR]),
+        "piece_blocks": int(h[_lib.PLAN_PIECE_BLOCKS]),
         "bt_rows": int(h[_lib.PLAN_BT_ROWS]),
         "bt_stride": int(h[_lib.PLAN_BT_STRIDE]),
         "max_blocks": int(h[_lib.PLAN_MAX_BLOCKS]),
         "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
-        # per worker: {first record, end record, <first record>, 0...}
-        "workers_table": table,
         "records": records,
-        "pieces": records[used] if used else records[:0],
-        "worker_start": np.concatenate([[0], np.cumsum(counts)]).astype(np.int64),
+        "pieces": records[used],
+        "record_index": np.nonzero(used)[0],
         # {kv head, first_slot, n_slots, row_start, q_len, 0 ...}
         "combines": words[oc:oc + PIECE_WORDS * n_comb].reshape(n_comb, PIECE_WORDS),
     }
@@ -148,17 +162,18 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
 
     device = torch.device(device)
     gqa = num_q_heads // num_kv_heads
-    if n_workers is None:
-        # size the grid for the row-tile count the grouping will produce
-        guess = min(64, gqa * max(1, (max_group_rows or 64) // gqa))
-        n_workers = num_workers(guess, device.index)
+    sized = n_workers is None
+    if sized:
+        # size the pieces for the row-tile count the grouping will produce
+        guess = min(MAX_GROUP_ROWS, gqa * max(1, (max_group_rows or MAX_GROUP_ROWS) // gqa))
+        n_workers = pieces_for(num_workers(guess, device.index), guess)
     words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim, block_size,
                            bt_rows, bt_stride, n_workers, max_group_rows)
     rows_max = int(words[_lib.PLAN_ROWS_MAX])
-    if rows_max > 0 and n_workers != num_workers(rows_max, device.index):
+    if sized and rows_max > 0 and n_workers != pieces_for(num_workers(rows_max, device.index), rows_max):
         words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim,
                                block_size, bt_rows, bt_stride,
-                               num_workers(rows_max, device.index), max_group_rows)
+                               pieces_for(num_workers(rows_max, device.index), rows_max), max_group_rows)
     # pinned and non-blocking: the upload does not wait for the stream
     # (the caching host allocator keeps the pinned block until the copy ran)
     src = torch.from_numpy(words)

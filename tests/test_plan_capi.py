@@ -68,8 +68,8 @@ def test_error_paths_without_gpu(lib):
     assert rc == 1 and "not a plan" in _lib.last_error()
 
 
-# planner constants (nebulasd_amd/csrc/nsd_common.h, nsd_host.cpp)
-MAX_WORKER_PIECES, MAX_WORKER_BLOCKS, MIN_PIECE_BLOCKS, PIECE_COST = 4, 1024, 4, 3
+# planner constants (nebulasd_amd/csrc/nsd_common.h)
+MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, MAX_SLOTS, XCDS, MAX_GROUP_ROWS = 256, 4, 128, 8, 48
 
 
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
@@ -83,98 +83,70 @@ def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows
 
 
 def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
-    groups, pieces, ws = p["groups"], p["pieces"], p["worker_start"]
+    groups, recs = p["groups"], p["records"]
     # groups tile the rows in order with seq_len rising by one inside a group
     r = 0
     for row_start, q_len, sid, ctx in groups:
-        assert row_start == r and q_len >= 1 and q_len * gqa <= 64
+        assert row_start == r and q_len >= 1 and q_len * gqa <= MAX_GROUP_ROWS
         for i in range(q_len):
             assert seq_ids[r + i] == sid and seq_lens[r + i] == ctx + 1 + i
         r += q_len
     assert r == len(seq_lens)
-    # segment = (group, kv head), in stream order; blocks of 16 tokens
-    seg_of = {(int(g[0]), h): i * hkv + h for i, g in enumerate(groups) for h in range(hkv)}
+    # segment = (group, kv head); blocks of 16 tokens
     nblk = [(-(-(int(g[3]) + int(g[1])) // 16)) for g in groups for _ in range(hkv)]
+    total = sum(nblk)
+    target = p["piece_blocks"]
+    want = max(MIN_PIECE_BLOCKS, -(-total // p["sized_for"]) if total else 0, -(-max(nblk, default=0) // MAX_SLOTS))
+    assert target == min(MAX_PIECE_BLOCKS, want)
+    # one workgroup per record, a multiple of the XCD count; each XCD's
+    # records (i, i + 8, ...) are its pieces longest first, empty ones last
+    assert len(recs) == p["workers"] and p["workers"] % XCDS == 0
+    seg_xcd, load = {}, [0] * XCDS
     covered = [np.zeros(n, int) for n in nblk]
-    last = (-1, -1)
-    for w in range(p["workers"]):
-        for pc in range(ws[w], ws[w + 1]):
-            h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, gend = (
-                int(x) for x in pieces[pc])
-            seg = seg_of[(row_start, h)]
+    pieces_of = {}
+    for x in range(XCDS):
+        mine = recs[x::XCDS]
+        live = mine[:, 5] > 0
+        n_live = int(live.sum())
+        assert live[:n_live].all(), "empty records only at the end of an XCD list"
+        sizes = (mine[:n_live, 2] - mine[:n_live, 1]).tolist()
+        assert sizes == sorted(sizes, reverse=True)
+        for rec in mine[:n_live]:
+            h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, seg = (int(v) for v in rec)
             g = groups[seg // hkv]
-            assert (q_len, sid, ctx) == (int(g[1]), int(g[2]), int(g[3]))
-            assert 0 <= bb < be <= nblk[seg]
-            assert (seg, bb) > last
-            last = (seg, be - 1)
+            assert h == seg % hkv and (row_start, q_len, sid, ctx) == tuple(int(v) for v in g)
+            assert 0 <= bb < be <= nblk[seg] and be - bb <= MAX_PIECE_BLOCKS
+            assert seg_xcd.setdefault(seg, x) == x, "a segment's pieces share one XCD"
             covered[seg][bb:be] += 1
+            load[x] += be - bb
+            pieces_of.setdefault(seg, []).append((bb, be, slot, comb, cfirst, cslots))
+        for rec in mine[n_live:]:
+            assert int(rec[5]) == 0 and int(rec[3]) == -1
     assert all((c == 1).all() for c in covered)
-    # slots exactly for segments cut into several pieces
-    per_seg = {}
-    for pcs in pieces:
-        per_seg.setdefault((int(pcs[4]), int(pcs[0])), []).append(int(pcs[3]))
+    if nblk:
+        assert max(load) - min(load) <= max(nblk)
+    assert p["max_blocks"] == max((int(r[2] - r[1]) for r in p["pieces"]), default=0)
+    # near-equal pieces per segment, ceil(blocks / target) of them; partial
+    # slots in segment order exactly for segments cut into several pieces
     combined = {(int(c[3]), int(c[0])): (int(c[1]), int(c[2])) for c in p["combines"]}
-    for key, slots in per_seg.items():
-        assert len(slots) <= 128
-        if len(slots) == 1:
-            assert slots == [-1] and key not in combined
+    next_slot = 0
+    for seg in sorted(pieces_of):
+        ps = sorted(pieces_of[seg])
+        k = -(-nblk[seg] // target)
+        assert len(ps) == k <= MAX_SLOTS
+        sizes = [be - bb for bb, be, *_ in ps]
+        assert max(sizes) - min(sizes) <= 1
+        key = (int(groups[seg // hkv][0]), seg % hkv)
+        if k == 1:
+            assert ps[0][2:] == (-1, -1, 0, 0) and key not in combined
         else:
             first, n = combined[key]
-            assert slots == list(range(first, first + n))
-    # each piece of a split segment names its combine record and slot range
-    for pcs in pieces:
-        comb, cfirst, cslots = int(pcs[8]), int(pcs[9]), int(pcs[10])
-        if int(pcs[3]) < 0:
-            assert (comb, cfirst, cslots) == (-1, 0, 0)
-        else:
-            c = p["combines"][comb]
-            assert (int(c[3]), int(c[0])) == (int(pcs[4]), int(pcs[0]))
-            assert (cfirst, cslots) == (int(c[1]), int(c[2]))
-            assert cfirst <= int(pcs[3]) < cfirst + cslots
-    # records sit at a fixed stride per worker (zero records in the gaps);
-    # the worker table holds each worker's record range and first record
-    stride, recs = p["piece_stride"], p["records"]
-    assert len(recs) == p["workers"] * stride
-    for w in range(p["workers"]):
-        row = p["workers_table"][w]
-        n = ws[w + 1] - ws[w]
-        assert (row[0], row[1]) == (w * stride, w * stride + n) and n <= stride
-        assert (recs[w * stride:w * stride + n] == pieces[ws[w]:ws[w + 1]]).all()
-        assert (recs[w * stride + n:(w + 1) * stride] == 0).all()
-        if n:
-            assert list(row[2:14]) == list(pieces[ws[w]])
-    # each record counts the blocks of its worker's earlier pieces (the offset
-    # of its block ids in the worker's id list)
-    blocks = []
-    for w in range(p["workers"]):
-        run = 0
-        for pc in range(ws[w], ws[w + 1]):
-            assert int(pieces[pc][11]) == run
-            run += int(pieces[pc][2] - pieces[pc][1])
-        blocks.append(run)
-    assert p["max_blocks"] == max(blocks)
-    # planner limits: pieces and blocks per worker
-    for w in range(p["workers"]):
-        assert ws[w + 1] - ws[w] <= MAX_WORKER_PIECES and blocks[w] <= MAX_WORKER_BLOCKS
-    # near-equal cost per active worker within each dispatch half (blocks
-    # plus 3 per piece; the first half's cap 1.5% above the second's); only
-    # the last active worker, or one stopped by the piece or block limit,
-    # may fall short
-    cost = [sum(int(pieces[pc][2] - pieces[pc][1]) + PIECE_COST for pc in range(ws[w], ws[w + 1]))
-            for w in range(p["workers"])]
-    active = [w for w in range(p["workers"]) if cost[w] > 0]
-    half = p.get("requested_workers", p["workers"]) // 2
-    for part in ([w for w in active if w < half], [w for w in active if w >= half]):
-        if not part:
-            continue
-        top = max(cost[w] for w in part)
-        for w in part:
-            if w == active[-1]:
-                continue
-            assert cost[w] >= top - (PIECE_COST + MIN_PIECE_BLOCKS) or \
-                ws[w + 1] - ws[w] == MAX_WORKER_PIECES or blocks[w] == MAX_WORKER_BLOCKS, \
-                (w, cost[w], top)
-    assert p["workers"] % 8 == 0
+            assert (first, n) == (next_slot, k)
+            assert [x[2] for x in ps] == list(range(first, first + k))
+            assert all(x[4:] == (first, k) for x in ps)
+            assert all(p["combines"][x[3]][0] == seg % hkv for x in ps)
+            next_slot += k
+    assert p["slots"] == next_slot
 
 
 def test_plan_caps_pieces_per_segment(lib):
@@ -220,11 +192,12 @@ def test_plan_invariants_random(lib, seed):
 
 
 def test_plan_splits_long_groups(lib):
-    # q_len 20 with GQA 4 -> 80 rows > 64: split into 16 + 4
+    # q_len 20 with GQA 4 -> 80 rows > 48: split into 12 + 8
     lens = list(range(501, 521))
     p, _ = _plan([0] * 20, lens)
-    assert p["groups"].tolist() == [[0, 16, 0, 500], [16, 4, 0, 516]]
-    assert p["rows_max"] == 64
+    assert p["groups"].tolist() == [[0, 12, 0, 500], [12, 8, 0, 512]]
+    assert p["rows_max"] == 48
+    check_plan_invariants(p, [0] * 20, lens, 8, 4)
 
 
 @pytest.mark.parametrize("bad", [
@@ -289,19 +262,30 @@ def test_qwen3_shape_constants():
 
 
 def test_plan_respects_kernel_limits(lib):
-    # thousands of one-block segments: at most 32 pieces per worker, so the
-    # plan grows past the requested 8 workers
+    # thousands of one-block segments: one piece each, no partials
     n = 2000
-    p, _ = _plan(list(range(n)), [1] * n, hq=16, hkv=8, workers=8, bt_rows=n, stride=16)
+    p, ws = _plan(list(range(n)), [1] * n, hq=16, hkv=8, workers=8, bt_rows=n, stride=16)
     check_plan_invariants(p, list(range(n)), [1] * n, 8, 2)
-    assert p["workers"] > 8
-    # one long request asked onto one worker: no worker streams more than
-    # 1024 blocks (its LDS id list), so the 8 x 4000 blocks take 32 workers
+    assert len(p["pieces"]) == n * 8 and ws == 0 and len(p["combines"]) == 0
+    # one long request asked onto one slot: pieces stop at 256 blocks (four
+    # waves, one block id per lane), so 4000 blocks take 16 pieces per kv head
     p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
-    assert p["max_blocks"] == MAX_WORKER_BLOCKS
-    assert sum(1 for w in range(p["workers"]) if p["worker_start"][w + 1] > p["worker_start"][w]) \
-        == 32
+    assert p["piece_blocks"] == MAX_PIECE_BLOCKS and p["max_blocks"] <= MAX_PIECE_BLOCKS
+    assert len(p["pieces"]) == 8 * 16
+
+
+def test_plan_xcd_lists_balance(lib):
+    # the verify shape: 16 requests x 8 kv heads over 8 XCDs, equal blocks per XCD
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(256, 4097, 16)
+    sid = [i for i in range(16) for _ in range(5)]
+    sl = [int(c) + 1 + k for c in ctx for k in range(5)]
+    p, _ = _plan(sid, sl, workers=1000, bt_rows=16)
+    check_plan_invariants(p, sid, sl, 8, 4)
+    recs = p["records"]
+    loads = [int((recs[x::8, 2] - recs[x::8, 1])[recs[x::8, 5] > 0].sum()) for x in range(8)]
+    assert max(loads) - min(loads) <= max(-(-(int(c) + 5) // 16) for c in ctx)
 
 
 def _attention_with_plan(lib, words, hq=32, hkv=8, bt_rows=2, bt_stride=4096):
@@ -341,12 +325,14 @@ def test_attention_rejects_corrupt_plans(lib):
 
     cases = [
         (corrupt(_lib.PLAN_MAX_BLOCKS, 0), "header"),
-        (corrupt(_lib.PLAN_PIECE_STRIDE, 0), "header"),
+        (corrupt(_lib.PLAN_MAX_BLOCKS, 257), "header"),
         (corrupt(_lib.PLAN_PIECES, int(h[_lib.PLAN_PIECES]) + 1), "header"),
-        (corrupt(op + 11, words[op + 11] + 1), "piece 0"),                      # block offset
+        (corrupt(_lib.PLAN_WORKERS, int(h[_lib.PLAN_WORKERS]) + 8), "header"),
+        (corrupt(op + 2, words[op + 1] + 257), "piece 0"),                      # > 256 blocks
         (corrupt(op + 6, 2), "piece 0"),                                        # seq_id past the table
         (corrupt(op + 2, 4096 * 2), "piece 0"),                                 # past the block table row
         (corrupt(op + 5, 64), "piece 0"),                                       # q_len * gqa > rows_max
+        (corrupt(op + 7, -1), "piece 0"),                                       # negative context
         (corrupt(op + PIECE_WORDS * split + 3, int(h[_lib.PLAN_SLOTS])), f"piece {split}"),
         (corrupt(op, 8), "piece 0"),                                            # kv head
     ]
