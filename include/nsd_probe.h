@@ -80,6 +80,14 @@ int nsd_probe_gather_wave(const void* k_cache, const void* v_cache, int64_t cach
                           int n_pieces, int round_tiles, int k_mode, int v_mode, int lds_extra,
                           uint32_t* sink, void* stream);
 
+/*
+ * nsd_probe_atomics: lane 0 of each of `grid` workgroups adds 1 to a device
+ * int32 counter `per_wg` (<= 4096) times, each add waiting for the previous
+ * result; one counter for the grid (spread 0), one per XCD (1) or one per
+ * workgroup (2, up to 1024 counters).  counters: device int32 [1024 * 64].
+ */
+int nsd_probe_atomics(int32_t* counters, int per_wg, int spread, int grid, uint32_t* sink, void* stream);
+
 /* nsd_probe_empty: launch a kernel of `grid` one-wave workgroups that does nothing. */
 int nsd_probe_empty(int grid, void* stream);
 

@@ -117,6 +117,7 @@ SIGNATURES = {
     "nsd_probe_gather_vgpr": (
         c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "nsd_probe_empty": (c_int, [c_int, c_void_p]),
+    "nsd_probe_atomics": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "nsd_probe_gather_wave": (
         c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int, c_int,
                 c_void_p, c_void_p]),

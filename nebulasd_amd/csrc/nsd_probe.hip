@@ -326,6 +326,21 @@ __global__ __launch_bounds__(kGatherThreads) void gather_wave_kernel(
   if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9e3779b9u) sink[0] = acc[0];
 }
 
+// Lane 0 of every workgroup adds 1 to a counter `per_wg` times in a row,
+// each add waiting for the previous one's result: one counter for the whole
+// grid (spread 0), one per XCD (spread 1, by blockIdx.x % 8), or one per
+// workgroup (spread 2); counters sit 256 bytes apart.  Measures the round
+// trip and the same-address throughput of device-scope atomics.
+__global__ void atomics_kernel(int32_t* ctrs, int per_wg, int spread, uint32_t* sink) {
+  if (threadIdx.x != 0) return;
+  const int slot = spread == 0 ? 0 : spread == 1 ? (int)(blockIdx.x % 8) : (int)(blockIdx.x % 1024);
+  int32_t* c = ctrs + 64 * slot;
+  int v = 0;
+  for (int i = 0; i < per_wg; ++i)
+    v += __hip_atomic_fetch_add(c, 1 + (v & 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (v == 0x7fffffff) sink[0] = (uint32_t)v;
+}
+
 }  // namespace
 }  // namespace nsd
 
@@ -448,6 +463,15 @@ extern "C" int nsd_probe_stream_read_unroll(const void* src, int64_t bytes, uint
     default: return fail(NSD_ERR_INVALID, "nsd_probe_stream_read: unroll %d not in {1, 2, 4, 8, 16}", unroll);
   }
   return launch_status("nsd_probe_stream_read");
+}
+
+extern "C" int nsd_probe_atomics(int32_t* counters, int per_wg, int spread, int grid, uint32_t* sink,
+                                 void* stream) {
+  if (counters == nullptr || sink == nullptr) return fail(NSD_ERR_INVALID, "nsd_probe_atomics: null pointer");
+  if (per_wg < 0 || per_wg > 4096 || spread < 0 || spread > 2 || grid <= 0 || grid > (1 << 20))
+    return fail(NSD_ERR_INVALID, "nsd_probe_atomics: argument out of range");
+  hipLaunchKernelGGL(atomics_kernel, dim3(grid), dim3(64), 0, as_stream(stream), counters, per_wg, spread, sink);
+  return launch_status("nsd_probe_atomics");
 }
 
 extern "C" int nsd_probe_empty(int grid, void* stream) {
