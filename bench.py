@@ -999,8 +999,10 @@ STREAM_PROBE_BYTES = 4 << 30
 
 
 def stream_read_probe(steps: int) -> dict:
-    """Contiguous read of a 4 GiB buffer (nsd_probe_stream_read): the device's
-    sequential-read rate, mean over `steps` graph replays."""
+    """Contiguous read of a 4 GiB buffer (nsd_probe_stream_read_unroll): the
+    device's sequential-read rate, swept over the grid (1-16 workgroups per
+    CU) and the 16-byte loads in flight per thread (1, 4, 8); each point is
+    the mean over `steps` graph replays.  `gbps` is the best point."""
     import torch
 
     from nebulasd_amd import _lib
@@ -1008,16 +1010,43 @@ def stream_read_probe(steps: int) -> dict:
     buf = torch.empty(STREAM_PROBE_BYTES // 2, dtype=torch.float16, device="cuda")
     buf.normal_()
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    grid = 16 * torch.cuda.get_device_properties(0).multi_processor_count
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sweep = []
+    for unroll in (1, 4, 8):
+        for per_cu in (1, 2, 4, 8, 16):
+            grid = per_cu * cus
 
-    def one():
-        _lib.call("nsd_probe_stream_read", buf.data_ptr(), STREAM_PROBE_BYTES, sink.data_ptr(), grid,
-                  torch.cuda.current_stream().cuda_stream)
-    us, per = _time_graph(one, torch.cuda.Stream(), max(3, steps), 2)
+            def one(grid=grid, unroll=unroll):
+                _lib.call("nsd_probe_stream_read_unroll", buf.data_ptr(), STREAM_PROBE_BYTES, sink.data_ptr(),
+                          grid, unroll, torch.cuda.current_stream().cuda_stream)
+            us, _ = _time_graph(one, torch.cuda.Stream(), max(3, steps), 2)
+            sweep.append({"grid": grid, "unroll": unroll, "us": us, "gbps": STREAM_PROBE_BYTES / us / 1e3})
     del buf
     torch.cuda.empty_cache()
-    return {"bytes": STREAM_PROBE_BYTES, "us": us, "gbps": STREAM_PROBE_BYTES / us / 1e3,
-            "frac_of_peak": STREAM_PROBE_BYTES / us / 1e3 / HBM_PEAK_GBPS}
+    best = max(sweep, key=lambda r: r["gbps"])
+    return {"bytes": STREAM_PROBE_BYTES, "us": best["us"], "gbps": best["gbps"],
+            "frac_of_peak": best["gbps"] / HBM_PEAK_GBPS, "best": dict(best), "sweep": sweep}
+
+
+def empty_launch_probe(steps: int) -> dict:
+    """A kernel that does nothing (nsd_probe_empty), 36 launches per graph
+    replay: the cost of one more launch inside a captured forward, for one
+    workgroup and for a grid of two per CU."""
+    import torch
+
+    from nebulasd_amd import _lib
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = {}
+    for name, grid in (("one_workgroup", 1), ("two_per_cu", 2 * cus)):
+        def one(grid=grid):
+            st = torch.cuda.current_stream().cuda_stream
+            for _ in range(36):
+                _lib.call("nsd_probe_empty", grid, st)
+        us, _ = _time_graph(one, torch.cuda.Stream(), max(5, steps), 2)
+        out[name] = us / 36
+    out["us_per_launch"] = out["two_per_cu"]
+    return out
 
 
 def attention_tiles(w, layer: int):
@@ -1036,42 +1065,129 @@ def attention_tiles(w, layer: int):
                            for sid, nb in need.items() for h in range(hkv)])
 
 
-def tile_gather_probe(w, steps: int, warmup: int) -> dict:
-    """The K/V tiles that workload `w`'s attention reads, gathered through an
-    LDS ring with no arithmetic (nsd_probe_tile_gather), split evenly over
-    two workgroups per CU, one launch per layer over all layers: the
-    attention's K/V read floor on this device."""
+def attention_segments(w) -> list:
+    """(first tile, tiles) of every (sequence, kv head) segment, in the order
+    of attention_tiles."""
+    bs, hkv = w.k_cache.shape[3], w.k_cache.shape[2]
+    need = {}
+    for sid, n in zip(w.seq_ids, w.seq_lens):
+        need[sid] = max(need.get(sid, 0), (int(n) + bs - 1) // bs)
+    segs, pos = [], 0
+    for nb in need.values():
+        for _ in range(hkv):
+            segs.append((pos, nb))
+            pos += nb
+    return segs
+
+
+def chunk_pieces(segs, chunk: int) -> list:
+    """Every segment cut into near-equal pieces of at most `chunk` tiles,
+    longest first (as the hardware then dispatches them)."""
+    import numpy as np
+
+    pieces = []
+    for s, n in segs:
+        k = -(-n // chunk)
+        cuts = np.rint(np.linspace(0, n, k + 1)).astype(int)
+        pieces += [(s + int(a), s + int(b)) for a, b in zip(cuts[:-1], cuts[1:])]
+    pieces.sort(key=lambda p: -(p[1] - p[0]))
+    return pieces
+
+
+# LDS pad that leaves `per_cu` workgroups of the given LDS use on one CU.
+def _lds_pad(base: int, per_cu: int) -> int:
+    return max(0, {2: 80, 3: 53, 4: 40}[per_cu] * 1024 - base)
+
+
+# The gather mechanisms of gather_probes: name -> (probe, pieces, arguments).
+# "split" cuts the tile stream evenly over two workgroups per CU; "chunkN"
+# cuts every segment into pieces of at most N tiles.
+GATHER_PROBES = {
+    "lds_ring_2_per_cu": ("tile_gather", "split", ()),
+    "lds_ring_3_per_cu": ("gather_pieces", "chunk8", ("ring", 6, 3)),
+    "lds_ring_4_per_cu": ("gather_pieces", "chunk4", ("ring", 4, 4)),
+    "registers": ("gather_vgpr", "chunk8", (1,)),
+    "wave_private_registers": ("gather_wave", "chunk16", (1, 0, 0, 0)),
+    "wave_private_lds_dma_2_per_cu": ("gather_wave", "chunk16", (1, 0, 1, 2)),
+}
+
+
+def gather_probes(w, steps: int, warmup: int) -> dict:
+    """The K/V tiles that workload `w`'s attention reads, one launch per
+    layer over all layers, gathered with no arithmetic by each mechanism of
+    GATHER_PROBES: an LDS ring filled by DMA at 2, 3 and 4 workgroups per CU,
+    16-byte loads straight into registers, and waves streaming on their own
+    (no barriers) into registers or into a double buffer of their own in LDS
+    (the attention kernel's mechanism).  The fastest is the attention's K/V
+    read floor on this device (`us_per_layer_call`, `gbps`)."""
     import numpy as np
     import torch
 
     from nebulasd_amd import _lib
 
     n_layers = w.k_cache.shape[1]
-    per_layer = [attention_tiles(w, layer) for layer in range(n_layers)]
-    n_tiles = len(per_layer[0])
-    workers = 2 * torch.cuda.get_device_properties(0).multi_processor_count
-    while -(-n_tiles // workers) > 1536:
-        workers *= 2
-    wstart = np.rint(np.linspace(0, n_tiles, workers + 1)).astype(np.int64)
+    base = np.stack([attention_tiles(w, layer) for layer in range(n_layers)])  # [L, n_tiles]
+    n_tiles = base.shape[1]
+    segs = attention_segments(w)
+    assert sum(n for _, n in segs) == n_tiles
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     dev = w.k_cache.device
-    tiles = torch.from_numpy(np.concatenate(per_layer)).to(dev)
-    wst = torch.from_numpy(wstart).to(dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    cache_elems = w.k_cache.numel()
-    assert int(tiles.max()) + 2048 <= cache_elems and int(tiles.min()) >= 0
-
-    def one_pass():
-        st = torch.cuda.current_stream().cuda_stream
-        for layer in range(n_layers):
-            _lib.call("nsd_probe_tile_gather", w.k_cache.data_ptr(), w.v_cache.data_ptr(), cache_elems,
-                      tiles.data_ptr() + layer * n_tiles * 8, n_tiles, wst.data_ptr(), workers,
-                      sink.data_ptr(), st)
-    us_pass, per = _time_graph(one_pass, torch.cuda.Stream(), max(1, steps), max(0, warmup))
-    us = us_pass / n_layers
+    ce = w.k_cache.numel()
+    assert int(base.max()) + 2048 <= ce and int(base.min()) >= 0
     kv_bytes = n_tiles * 2 * 2048 * w.k_cache.element_size()
-    return {"tiles_per_layer_call": n_tiles, "kv_bytes": kv_bytes, "workgroups": workers,
-            "us_per_layer_call": us, "us_per_layer_call_spread": _spread(per, n_layers),
-            "gbps": kv_bytes / us / 1e3, "frac_of_peak": kv_bytes / us / 1e3 / HBM_PEAK_GBPS}
+    out = {}
+    for name, (probe, split, extra) in GATHER_PROBES.items():
+        if split == "split":
+            workers = 2 * cus
+            while -(-n_tiles // workers) > 1536:
+                workers *= 2
+            starts = np.rint(np.linspace(0, n_tiles, workers + 1)).astype(np.int64)
+            order = np.arange(n_tiles)
+        else:
+            pieces = chunk_pieces(segs, int(split[5:]))
+            assert max(b - a for a, b in pieces) <= 256
+            order = np.concatenate([np.arange(a, b) for a, b in pieces])
+            starts = np.concatenate([[0], np.cumsum([b - a for a, b in pieces])]).astype(np.int64)
+        n_p = len(starts) - 1
+        tiles = torch.from_numpy(np.ascontiguousarray(base[:, order]).reshape(-1)).to(dev)
+        pst = torch.from_numpy(starts).to(dev)
+
+        def one_pass(probe=probe, extra=extra, tiles=tiles, pst=pst, n_p=n_p):
+            st = torch.cuda.current_stream().cuda_stream
+            for layer in range(n_layers):
+                tp = tiles.data_ptr() + layer * n_tiles * 8
+                common = (w.k_cache.data_ptr(), w.v_cache.data_ptr(), ce, tp, n_tiles, pst.data_ptr(), n_p)
+                if probe == "tile_gather":
+                    _lib.call("nsd_probe_tile_gather", *common, sink.data_ptr(), st)
+                elif probe == "gather_pieces":
+                    ring, per_cu = extra[1], extra[2]
+                    _lib.call("nsd_probe_gather_pieces", *common, ring,
+                              _lds_pad(ring * 8192 + 2048, per_cu), sink.data_ptr(), st)
+                elif probe == "gather_vgpr":
+                    _lib.call("nsd_probe_gather_vgpr", *common, extra[0], sink.data_ptr(), st)
+                else:
+                    rnd, kmode, vmode, per_cu = extra
+                    pad = _lds_pad(2048 + 4 * 2 * rnd * 4096, per_cu) if vmode else 0
+                    _lib.call("nsd_probe_gather_wave", *common, rnd, kmode, vmode, pad, sink.data_ptr(), st)
+        us_pass, per = _time_graph(one_pass, torch.cuda.Stream(), max(1, steps), max(0, warmup))
+        us = us_pass / n_layers
+        out[name] = {"workgroups": n_p, "us_per_layer_call": us, "gbps": kv_bytes / us / 1e3}
+        del tiles, pst
+    best = min(out, key=lambda k: out[k]["us_per_layer_call"])
+    return {"tiles_per_layer_call": n_tiles, "kv_bytes": kv_bytes, "mechanisms": out,
+            "best": dict(out[best], mechanism=best), "us_per_layer_call": out[best]["us_per_layer_call"],
+            "gbps": out[best]["gbps"], "frac_of_peak": out[best]["gbps"] / HBM_PEAK_GBPS,
+            "same_mechanism_us": out["wave_private_lds_dma_2_per_cu"]["us_per_layer_call"]}
+
+
+def with_gather_floor(res: dict, w, steps: int, warmup: int) -> None:
+    """Adds the gather probes of workload `w` to its leg `res`: the floor,
+    the attention's fraction of it, and of the floor of its own mechanism."""
+    fl = gather_probes(w, steps, warmup)
+    res["kv_gather_floor"] = fl
+    res["frac_of_gather_floor"] = fl["us_per_layer_call"] / res["us_per_layer_call"]
+    res["frac_of_same_mechanism_floor"] = fl["same_mechanism_us"] / res["us_per_layer_call"]
 
 
 def measure_spec_loop(seed: int, steps: int, cpu_seconds: float) -> dict:
@@ -1260,7 +1376,8 @@ def _cpu_model() -> str:
 # full per-leg results go to stderr as one "# detail " JSON line.
 LINE_MAX_BYTES = 7500
 # Scalar figures a secondary leg keeps on the stdout line, when it has them.
-LEG_KEYS = ("us_per_layer_call", "hbm_gbps", "hbm_frac", "frac_of_gather_floor", "tflops", "mfma_frac",
+LEG_KEYS = ("us_per_layer_call", "hbm_gbps", "hbm_frac", "frac_of_gather_floor", "frac_of_same_mechanism_floor",
+            "tflops", "mfma_frac",
             "us_per_write", "reference_us_per_write", "us_per_layer", "floor_us_at_copy_rate",
             "reference_sdpa_loop_us", "us_per_call", "reference_us_per_call", "us_per_call_graph")
 # Second-level dicts of a leg whose scalar figures are kept as well.
@@ -1298,6 +1415,12 @@ def compact_leg(r: dict) -> dict:
                 s2 = _scalars(v2, ("decode_tokens_per_s", "us_per_layer", "us_per_call"))
                 if s2:
                     s[k2] = s2
+        if sub == "kv_gather_floor":  # the floor's mechanism and every mechanism's time
+            if isinstance(v.get("best"), dict):
+                s["best"] = v["best"].get("mechanism")
+            if isinstance(v.get("mechanisms"), dict):
+                s["mechanisms_us"] = {k2: _sig(m.get("us_per_layer_call")) for k2, m in v["mechanisms"].items()
+                                      if isinstance(m, dict)}
         if s:
             out[sub] = s
     for k, v in r.items():  # rest-of-layer legs: one dict per kernel and shape
@@ -1371,12 +1494,14 @@ def main():
     probes = {"copy_gbps": copy_gbps}
     if args.probes:
         probes["stream_read"] = stream_read_probe(args.steps)
-        print(f"# probes: contiguous read {probes['stream_read']['gbps']:.0f} GB/s, copy {copy_gbps:.0f} GB/s",
-              file=sys.stderr, flush=True)
+        probes["empty_launch_in_graph"] = empty_launch_probe(args.steps)
+        print(f"# probes: contiguous read {probes['stream_read']['gbps']:.0f} GB/s "
+              f"(grid {probes['stream_read']['best']['grid']}, {probes['stream_read']['best']['unroll']} loads "
+              f"in flight), copy {copy_gbps:.0f} GB/s, empty launch in a graph "
+              f"{probes['empty_launch_in_graph']['us_per_launch']:.2f} us", file=sys.stderr, flush=True)
     res, w = measure(args.workload, args.seed, args.steps, args.warmup)
     if args.probes:
-        res["kv_gather_floor"] = tile_gather_probe(w, args.steps, args.warmup)
-        res["frac_of_gather_floor"] = res["kv_gather_floor"]["us_per_layer_call"] / res["us_per_layer_call"]
+        with_gather_floor(res, w, args.steps, args.warmup)
     print(f"# {args.workload}: {res['us_per_layer_call']:.2f} us/layer-call, "
           f"{res['hbm_gbps']:.0f} GB/s" + (f" (K/V gather floor {res['kv_gather_floor']['us_per_layer_call']:.2f} us)"
                                           if args.probes else ""), file=sys.stderr, flush=True)
@@ -1444,8 +1569,7 @@ def main():
     for name in filter(None, args.secondary.split(",")):
         r2, w2 = measure(name, args.seed, args.steps, args.warmup)
         if args.probes:
-            r2["kv_gather_floor"] = tile_gather_probe(w2, args.steps, args.warmup)
-            r2["frac_of_gather_floor"] = r2["kv_gather_floor"]["us_per_layer_call"] / r2["us_per_layer_call"]
+            with_gather_floor(r2, w2, args.steps, args.warmup)
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
               f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
         if args.cpu_baseline_seconds > 0:

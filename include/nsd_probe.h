@@ -2,9 +2,10 @@
  * Measurement probes beside the attention path: the HBM read rates that bound
  * the paged attention on this device.  They have no counterpart in the
  * reference (whose path is Triton kernels with no ceiling measurement); the
- * benchmark reports them next to the attention's achieved rate.  Both read
- * device memory only and write one word of `sink` only in a case the data
- * practically never meets (it keeps the loads from being optimised away).
+ * benchmark reports them next to the attention's achieved rate.  The read
+ * probes read device memory only and write one word of `sink` only in a case
+ * the data practically never meets (it keeps the loads from being optimised
+ * away).
  * Return codes as in nsd_attn.h.
  */
 #ifndef NSD_PROBE_H
@@ -72,8 +73,8 @@ int nsd_probe_gather_vgpr(const void* k_cache, const void* v_cache, int64_t cach
  * round in flight.  k_mode 1 reads K in the A-operand layout of
  * v_mfma_f32_16x16x32_f16 (16 rows x 64 B per load), 0 in contiguous 1 KB
  * runs; v_mode 0 reads V into registers, 1 into the wave's own LDS slots by
- * global_load_lds_dwordx4.  LDS: 2 KiB + (v_mode ? 64 KiB * round_tiles : 0)
- * + lds_extra bytes per workgroup.
+ * global_load_lds_dwordx4.  LDS: 2 KiB + (v_mode ? 32 KiB * round_tiles : 0)
+ * + lds_extra bytes per workgroup (at most 160 KiB).
  */
 int nsd_probe_gather_wave(const void* k_cache, const void* v_cache, int64_t cache_elems,
                           const int64_t* tiles, int64_t n_tiles, const int64_t* piece_start,

@@ -33,11 +33,11 @@ enum PlanHeader {
   kPlanHq,
   kPlanHkv,
   kPlanOffGroups,      // word offset of groups [n_groups][4] {row_start, q_len, seq_id, ctx}
-  kPlanSizedFor,       // the n_workers (wave slots) the piece size was chosen for
+  kPlanSizedFor,       // the n_workers (pieces asked for) the plan was cut for
   kPlanOffPieces,      // word offset of pieces [n_pieces][kPieceWords]
   kPlanOffCombines,    // word offset of combines [n_combines][kPieceWords]
   kPlanWords,          // total words
-  kPlanPieceBlocks,    // target blocks per piece
+  kPlanPieceBlocks,    // mean blocks per piece, rounded up
   kPlanBtRows,         // block-table rows every piece's seq_id was checked against
   kPlanBtStride,       // block-table row length every piece's block range was checked against
   kPlanMaxBlocks,      // most 16-token blocks in one piece

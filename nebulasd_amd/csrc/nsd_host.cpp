@@ -103,54 +103,77 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   }
   const int64_t total = seg_start[n_segs];
 
-  // 3. pieces: every segment is cut into near-equal pieces of about
-  //    `target` blocks, where target spreads the stream over the n_workers
-  //    wave slots (at least kMinPieceBlocks, at most kMaxPieceBlocks, and
-  //    few enough pieces per segment for kMaxSlotsPerSegment partials).
-  int64_t max_seg = 0;
-  for (int64_t s = 0; s < n_segs; ++s) max_seg = std::max(max_seg, seg_start[s + 1] - seg_start[s]);
-  int64_t target = total > 0 ? (total + n_workers - 1) / n_workers : kMinPieceBlocks;
-  target = std::max<int64_t>(target, kMinPieceBlocks);
-  target = std::max<int64_t>(target, (max_seg + kMaxSlotsPerSegment - 1) / kMaxSlotsPerSegment);
-  target = std::min<int64_t>(target, kMaxPieceBlocks);
-  if ((max_seg + target - 1) / target > kMaxSlotsPerSegment)
-    return fail(NSD_ERR_UNSUPPORTED, "plan: a segment of %lld blocks needs more than %d pieces of %d",
-                (long long)max_seg, kMaxSlotsPerSegment, kMaxPieceBlocks);
+  // 3. pieces per segment.  Every segment starts with the fewest pieces of
+  //    at most kMaxPieceBlocks blocks; then, while the plan has fewer than
+  //    n_workers pieces, one more piece goes to the segment whose pieces are
+  //    the longest (ties: the lower segment), as long as its pieces stay at
+  //    least kMinPieceBlocks long and it stays within kMaxSlotsPerSegment.
+  //    No cut into that many pieces has a shorter longest piece, and with
+  //    n_workers = the device's workgroup slots every piece starts at once.
   std::vector<int64_t> seg_pieces(n_segs);
+  int64_t n_pieces = 0;
   for (int64_t s = 0; s < n_segs; ++s) {
     const int64_t nb = seg_start[s + 1] - seg_start[s];
-    seg_pieces[s] = (nb + target - 1) / target;
+    seg_pieces[s] = std::max<int64_t>(1, (nb + kMaxPieceBlocks - 1) / kMaxPieceBlocks);
+    if (seg_pieces[s] > kMaxSlotsPerSegment)
+      return fail(NSD_ERR_UNSUPPORTED, "plan: a segment of %lld blocks needs more than %d pieces of %d",
+                  (long long)nb, kMaxSlotsPerSegment, kMaxPieceBlocks);
+    n_pieces += seg_pieces[s];
   }
-
-  // 4. segments to XCDs (workgroup i runs on XCD i % 8): longest first, each
-  //    to the XCD with the fewest blocks so far, so a segment's pieces share
-  //    one L2 (its query rows) and every XCD gets near-equal work.  Each
-  //    XCD's pieces then go longest first, so the shortest come last.
-  std::vector<int64_t> order(n_segs);
-  for (int64_t s = 0; s < n_segs; ++s) order[s] = s;
-  std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) {
-    return seg_start[x + 1] - seg_start[x] > seg_start[y + 1] - seg_start[y];
-  });
-  std::vector<std::vector<std::pair<int64_t, int64_t>>> lists(kXcds);  // (segment, piece index)
-  std::vector<int64_t> load(kXcds, 0);
-  for (int64_t s : order) {
-    const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-    load[x] += seg_start[s + 1] - seg_start[s];
-    for (int64_t k = 0; k < seg_pieces[s]; ++k) lists[x].push_back({s, k});
+  {
+    // max-heap on blocks per piece, nb_s / n_s, compared without division
+    auto shorter = [&](int64_t x, int64_t y) {
+      const int64_t ax = (seg_start[x + 1] - seg_start[x]) * seg_pieces[y];
+      const int64_t ay = (seg_start[y + 1] - seg_start[y]) * seg_pieces[x];
+      return ax != ay ? ax < ay : x > y;
+    };
+    std::vector<int64_t> heap;
+    for (int64_t s = 0; s < n_segs; ++s) heap.push_back(s);
+    std::make_heap(heap.begin(), heap.end(), shorter);
+    while (n_pieces < n_workers && !heap.empty()) {
+      std::pop_heap(heap.begin(), heap.end(), shorter);
+      const int64_t s = heap.back();
+      heap.pop_back();
+      const int64_t nb = seg_start[s + 1] - seg_start[s], n = seg_pieces[s] + 1;
+      if (n > kMaxSlotsPerSegment || nb < n * kMinPieceBlocks) continue;  // cut as far as it goes
+      seg_pieces[s] = n;
+      ++n_pieces;
+      heap.push_back(s);
+      std::push_heap(heap.begin(), heap.end(), shorter);
+    }
   }
   auto piece_blocks = [&](int64_t s, int64_t k) {
     const int64_t nb = seg_start[s + 1] - seg_start[s], n = seg_pieces[s];
     return std::make_pair(k * nb / n, (k + 1) * nb / n);
   };
-  size_t longest = 0;
-  for (auto& l : lists) {
-    std::stable_sort(l.begin(), l.end(), [&](const std::pair<int64_t, int64_t>& x,
-                                            const std::pair<int64_t, int64_t>& y) {
-      const auto bx = piece_blocks(x.first, x.second), by = piece_blocks(y.first, y.second);
-      return bx.second - bx.first > by.second - by.first;
-    });
-    longest = std::max(longest, l.size());
+
+  // 4. pieces to XCDs (workgroup i runs on XCD i % 8): longest first (ties:
+  //    segment, then piece order), each to the XCD with the fewest blocks
+  //    among those holding fewer than ceil(pieces / 8), so the XCDs get
+  //    near-equal work and list lengths that differ by at most one.  Each
+  //    XCD's list is then longest first, as the hardware dispatches it.
+  std::vector<std::pair<int64_t, int64_t>> all;  // (segment, piece index)
+  all.reserve(n_pieces);
+  for (int64_t s = 0; s < n_segs; ++s)
+    for (int64_t k = 0; k < seg_pieces[s]; ++k) all.push_back({s, k});
+  std::stable_sort(all.begin(), all.end(), [&](const std::pair<int64_t, int64_t>& x,
+                                              const std::pair<int64_t, int64_t>& y) {
+    const auto bx = piece_blocks(x.first, x.second), by = piece_blocks(y.first, y.second);
+    return bx.second - bx.first > by.second - by.first;
+  });
+  const size_t cap = (size_t)((n_pieces + kXcds - 1) / kXcds);
+  std::vector<std::vector<std::pair<int64_t, int64_t>>> lists(kXcds);
+  std::vector<int64_t> load(kXcds, 0);
+  for (const auto& pc : all) {
+    int x = -1;
+    for (int c = 0; c < kXcds; ++c)
+      if (lists[c].size() < cap && (x < 0 || load[c] < load[x])) x = c;
+    const auto b = piece_blocks(pc.first, pc.second);
+    load[x] += b.second - b.first;
+    lists[x].push_back(pc);
   }
+  const size_t longest = n_pieces > 0 ? cap : 0;
+  const int64_t target = n_pieces > 0 ? (total + n_pieces - 1) / n_pieces : 0;
 
   // 5. partial slots for segments cut into several pieces, in segment order.
   std::vector<int32_t> combines;  // kPieceWords per record

@@ -11,7 +11,10 @@ def _big_leg(i: int) -> dict:
                          "samples": list(range(50)), "note": "x" * 200} for j in range(20)}
     return dict(sub, workload=f"leg{i}", us_per_layer_call=12.345678, hbm_gbps=4321.0, hbm_frac=0.54,
                 frac_of_gather_floor=0.9, spread={"p10": 1.0, "p90": 2.0, "list": list(range(500))},
-                kv_gather_floor={"us_per_layer_call": 11.1, "gbps": 5000.0, "spread": list(range(100))},
+                kv_gather_floor={"us_per_layer_call": 11.1, "gbps": 5000.0, "spread": list(range(100)),
+                                 "best": {"mechanism": "registers", "us_per_layer_call": 11.1},
+                                 "mechanisms": {f"mech_{j}": {"us_per_layer_call": 11.1 + j, "workgroups": 512,
+                                                              "gbps": 5000.0} for j in range(6)}},
                 cpu_baseline={"value": 1.5e5, "unit": "us/layer-call", "cores": 16, "kind": "port",
                               "sample": "y" * 300, "cpu_model": "z" * 50},
                 throughput={"native": {"decode_tokens_per_s": 2800.0, "wall_s": 10.0}},
@@ -29,6 +32,8 @@ def _line() -> dict:
         "cpu_baseline": {"value": 7.8e4, "unit": "us/layer-call", "cores": 16, "kind": "port",
                          "sample": "20 layer calls"},
         "probes": bench._compact_probes({"copy_gbps": 5000.0,
+                                         "empty_launch_in_graph": {"one_workgroup": 1.8, "two_per_cu": 1.9,
+                                                                   "us_per_launch": 1.9},
                                          "stream_read": {"gbps": 6100.0, "us": 700.0,
                                                          "sweep": [{"gbps": 1.0}] * 100,
                                                          "best": {"gbps": 6200.0, "grid": 1024, "unroll": 8}}}),
@@ -46,6 +51,7 @@ def test_stdout_line_fits_and_parses():
     assert parsed["roofline"]["traffic"] == 1.6e8
     assert parsed["probes"]["stream_read"]["best"]["grid"] == 1024
     assert "sweep" not in parsed["probes"]["stream_read"]
+    assert parsed["probes"]["empty_launch_in_graph"]["us_per_launch"] == 1.9
 
 
 def test_compact_leg_keeps_headline_figures():
@@ -53,6 +59,8 @@ def test_compact_leg_keeps_headline_figures():
     assert leg["us_per_layer_call"] == 12.346
     assert leg["frac_of_gather_floor"] == 0.9
     assert leg["kv_gather_floor"]["us_per_layer_call"] == 11.1
+    assert leg["kv_gather_floor"]["best"] == "registers"
+    assert leg["kv_gather_floor"]["mechanisms_us"]["mech_5"] == 16.1
     assert leg["cpu_baseline"] == {"value": 1.5e5, "unit": "us/layer-call", "cores": 16, "kind": "port"}
     assert leg["throughput"]["native"]["decode_tokens_per_s"] == 2800.0
     assert "prompts" not in leg and "spread" not in leg
