@@ -214,6 +214,8 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
  * bytes than it holds is rejected with NSD_ERR_WORKSPACE.  The call
  * allocates nothing.  Every call on one GPU shares the array: calls that
  * overlap on one GPU (two streams, two threads) race and must not overlap.
+ * Issue them on one stream per GPU, or order the streams (an event between
+ * one call's stream and the next call's) -- the library does not check.
  * Same arguments, results and errors as nsd_paged_attention.
  */
 #define NSD_NOALLOC_SCRATCH_BYTES (16ll << 20)

@@ -294,13 +294,13 @@ int check_linear(int64_t n_rows, int64_t n_out, int64_t n_in, const char* who) {
 template <int MT, int TN>
 int launch_linear(const f16* x, const f16* w, float* part, int rows, int n, int k, int splits, hipStream_t st) {
   using S = LinearShape<MT, TN>;
-  static bool attr_set = false;  // per-process: raise the dynamic-LDS limit once
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_partials_kernel<MT, TN>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
-    if (e != hipSuccess) return fail(NSD_ERR_HIP, "linear: LDS attribute: %s", hipGetErrorString(e));
-    attr_set = true;
-  }
+  // raise the dynamic-LDS limit once per process: a function-local static is
+  // initialised exactly once even when several threads launch at once, and
+  // a failure stays reported on every later call
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&linear_partials_kernel<MT, TN>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      S::kLds);
+  if (attr != hipSuccess) return fail(NSD_ERR_HIP, "linear: LDS attribute: %s", hipGetErrorString(attr));
   const int n_tiles = n / TN;
   hipLaunchKernelGGL((linear_partials_kernel<MT, TN>), dim3(n_tiles * splits), dim3(kGemmThreads), S::kLds, st, x,
                      w, part, rows, n, k, splits, n_tiles, nullptr);
@@ -315,13 +315,10 @@ constexpr int kGatedMaxRowTiles = 7;  // three ring slots fit up to 112 rows (12
 template <int MT>
 int launch_gated(const f16* x, const f16* w, f16* y, int rows, int inter, int hidden, hipStream_t st) {
   using S = LinearShape<MT, kGatedTile, true>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_partials_kernel<MT, kGatedTile, true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
-    if (e != hipSuccess) return fail(NSD_ERR_HIP, "up_gate: LDS attribute: %s", hipGetErrorString(e));
-    attr_set = true;
-  }
+  static const hipError_t attr = hipFuncSetAttribute(  // once per process, as in launch_linear
+      reinterpret_cast<const void*>(&linear_partials_kernel<MT, kGatedTile, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
+  if (attr != hipSuccess) return fail(NSD_ERR_HIP, "up_gate: LDS attribute: %s", hipGetErrorString(attr));
   const int n_tiles = inter / (kGatedTile / 2);
   hipLaunchKernelGGL((linear_partials_kernel<MT, kGatedTile, true>), dim3(n_tiles), dim3(kGemmThreads), S::kLds, st,
                      x, w, nullptr, rows, inter, hidden, 1, n_tiles, y);

@@ -346,14 +346,12 @@ prefill_attn_kernel(PrefillArgs a) {
 
 template <class C>
 int launch_prefill(PrefillArgs args, hipStream_t stream) {
-  static bool attr_set = false;  // per-process: allow the dynamic LDS once
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<C>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::lds_bytes);
-    if (e != hipSuccess)
-      return fail(NSD_ERR_HIP, "prefill_attention: LDS attribute: %s", hipGetErrorString(e));
-    attr_set = true;
-  }
+  // allow the dynamic LDS once per process: a function-local static is
+  // initialised exactly once even when several threads launch at once, and
+  // a failure stays reported on every later call
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<C>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, C::lds_bytes);
+  if (attr != hipSuccess) return fail(NSD_ERR_HIP, "prefill_attention: LDS attribute: %s", hipGetErrorString(attr));
   args.positions = C::rows / args.gqa;
   args.q_blocks = (args.max_seqlen + args.positions - 1) / args.positions;
   const int64_t grid = (int64_t)args.q_blocks * args.n_seqs * args.hkv;

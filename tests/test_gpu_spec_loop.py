@@ -1,10 +1,11 @@
 """The speculative loop on random-init Qwen3-0.6B (draft) + Qwen3-8B (target).
 
-Runs at the single-GPU speculative configuration's shapes -- draft batch 64,
-target batch 16, depth 4, prompts U[128, 1024] -- with fewer requests and
-output tokens than the full 512 x 128 run, plus a reduced run and a run in
-which the draft holds the target's weights, so that proposals are accepted
-and the multi-token append and the draft's two-row reconcile step execute.
+Runs the full single-GPU speculative configuration (512 requests x 128
+generated tokens, draft batch 64, target batch 16, depth 4, prompts
+U[128, 1024]), the same shapes with fewer requests and tokens, a reduced run,
+and a run in which the draft holds the target's weights, so that proposals
+are accepted and the multi-token append and the draft's two-row reconcile
+step execute.
 Attention layer calls sampled from both models are checked against the
 oracle; every request must finish with exactly the requested tokens.
 """
@@ -35,6 +36,28 @@ def test_speculative_loop_small(gpu):
     # both models' calls were checked, verify rows (q_len 5) included
     assert {r["layers"] for r in results} == {28, 36}
     assert max(r["max_q_len"] for r in results if r["layers"] == 36) == 5
+
+
+def test_speculative_loop_full_configuration(gpu):
+    """The full single-GPU speculative configuration: 512 requests, prompts
+    U[128, 1024], 128 generated tokens each, draft batch 64, target batch 16,
+    depth 4, greedy.  Every 251st forward (a stride co-prime with the eight
+    forwards of a draft group, so draft decodes and target verifies are both
+    sampled) hands its mid-depth attention layer call to the oracle; every
+    request ends with exactly 128 tokens."""
+    results = []
+    res = run(n_requests=512, new_tokens=128, draft_batch=64, target_batch=16, depth=4, seed=0,
+              check_every=251, make_check=make_checker(results), device=gpu, return_outputs=True)
+    outputs = res.pop("outputs")
+    print({k: v for k, v in res.items()}, flush=True)
+    assert res["requests"] == 512 and res["generated_tokens"] == 512 * 128
+    assert len(outputs) == 512 and all(len(o) == 128 for o in outputs)
+    assert res["rounds"] <= 127 and res["target_forwards"] > 0 and res["draft_forwards"] > 0
+    assert len(results) == res["attention_checks"] >= 30
+    assert all(r["ok"] for r in results), [r for r in results if not r["ok"]]
+    assert {r["layers"] for r in results} == {28, 36}
+    assert max(r["rows"] for r in results if r["layers"] == 36) == 16 * 5
+    assert max(r["rows"] for r in results if r["layers"] == 28) == 64
 
 
 def test_speculative_loop_config_shape(gpu):

@@ -128,3 +128,79 @@ def test_capi_argument_checks_without_gpu():
     assert lib.nsd_lm_head_argmax(None, None, 0, 128, 10, None, None, None) == 0
     assert lib.nsd_argmax_rows(None, 0, 10, None, None) == 0
 
+
+
+def _tiny_layer(rng, hidden=32, hq=4, hkv=2, d=16, inter=24):
+    w = {"n_in": (rng.random(hidden) + 0.5).astype(np.float16),
+         "wqkv": _h(rng, (hq + 2 * hkv) * d, hidden, scale=0.2),
+         "q_norm": (rng.random(d) + 0.5).astype(np.float16),
+         "k_norm": (rng.random(d) + 0.5).astype(np.float16),
+         "wo": _h(rng, hidden, hq * d, scale=0.2),
+         "n_post": (rng.random(hidden) + 0.5).astype(np.float16),
+         "wug": _h(rng, 2 * inter, hidden, scale=0.2),
+         "wd": _h(rng, hidden, inter, scale=0.2)}
+    return w
+
+
+def _tiny_state(rng, seq_lens, hkv=2, d=16, n_blocks=12):
+    """Three sequences, one row each at the given lengths, their blocks a
+    shuffled pool; caches filled with noise (the rows' own slots included)."""
+    bt = rng.permutation(n_blocks).astype(np.int32).reshape(3, 4)
+    kc = _h(rng, n_blocks, 2, hkv, 16, d)
+    vc = _h(rng, n_blocks, 2, hkv, 16, d)
+    cos, sin = oracle.rope_cache(d, 10000.0, 64)
+    return bt, kc, vc, cos, sin, [0, 1, 2], list(seq_lens)
+
+
+def test_decoder_layer_zero_projections_pass_the_residual():
+    rng = np.random.default_rng(10)
+    w = _tiny_layer(rng)
+    w["wo"][:] = 0
+    w["wd"][:] = 0
+    bt, kc, vc, cos, sin, sids, slens = _tiny_state(rng, [5, 17, 40])
+    x, res = _h(rng, 3, 32), _h(rng, 3, 32)
+    y, r2 = oracle.decoder_layer(x, res, w, 1e-6, cos, sin, kc, vc, bt, sids, slens, 1, 4, 2)
+    assert (y == 0).all()
+    np.testing.assert_array_equal(r2, (torch.from_numpy(x) + torch.from_numpy(res)).numpy())
+
+
+def test_decoder_layer_first_tokens_closed_form():
+    """Every row is its sequence's first token: attention returns the row's
+    own v (one kv head per GQA group of q heads), so the residual out is
+    fp16(x + residual) + v repeated over the group times W_o; the V slot
+    holds the v rows of the stacked projection (rows q | k | v), and a
+    gate half of zeros zeroes the output (the gate is the second half)."""
+    rng = np.random.default_rng(11)
+    hidden, hq, hkv, d, inter = 32, 4, 2, 16, 24
+    w = _tiny_layer(rng)
+    bt, kc, vc, cos, sin, sids, slens = _tiny_state(rng, [1, 1, 1])
+    x, res = _h(rng, 3, hidden), _h(rng, 3, hidden)
+    w0 = {k: v.copy() for k, v in w.items()}
+    w0["wug"][inter:] = 0
+    kc0, vc0 = kc.copy(), vc.copy()
+    y, r2 = oracle.decoder_layer(x, res, w0, 1e-6, cos, sin, kc0, vc0, bt, sids, slens, 0, hq, hkv)
+    assert (y == 0).all()
+    r1 = (x.astype(np.float32) + res.astype(np.float32)).astype(np.float16)
+    xf = r1.astype(np.float64)
+    h = (xf / np.sqrt((xf * xf).mean(1, keepdims=True) + 1e-6) * w["n_in"].astype(np.float64)).astype(np.float16)
+    v = (h.astype(np.float64) @ w["wqkv"][(hq + hkv) * d:].astype(np.float64).T).astype(np.float16)
+    v = v.reshape(3, hkv, d)
+    for r in range(3):
+        np.testing.assert_array_equal(vc0[bt[r, 0], 0, :, 0], v[r])
+    o = np.repeat(v, hq // hkv, axis=1).reshape(3, hq * d)  # q head j reads kv head j // (hq / hkv)
+    a = (o.astype(np.float64) @ w["wo"].astype(np.float64).T).astype(np.float16)
+    want = (a.astype(np.float32) + r1.astype(np.float32)).astype(np.float16)
+    np.testing.assert_array_equal(r2, want)
+    # the same layer with the gate kept: a non-zero output, changed by a swap of the halves
+    y1, _ = oracle.decoder_layer(x, res, w, 1e-6, cos, sin, kc.copy(), vc.copy(), bt, sids, slens, 0, hq, hkv)
+    assert np.abs(y1.astype(np.float64)).max() > 0
+    ws = dict(w, wug=np.concatenate([w["wug"][inter:], w["wug"][:inter]]))
+    ys, _ = oracle.decoder_layer(x, res, ws, 1e-6, cos, sin, kc.copy(), vc.copy(), bt, sids, slens, 0, hq, hkv)
+    assert not np.array_equal(ys, y1)
+
+
+def test_decoder_layer_linear_matches_torch():
+    rng = np.random.default_rng(12)
+    x, wt = _h(rng, 5, 64), _h(rng, 48, 64, scale=0.1)
+    want = F.linear(torch.from_numpy(x).double(), torch.from_numpy(wt).double()).half().numpy()
+    np.testing.assert_array_equal(oracle.linear(x, wt), want)

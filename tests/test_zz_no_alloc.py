@@ -1,7 +1,8 @@
 """The allocation-free attention entry point against the workspace one.
 
-``nsd_paged_attention_noalloc`` keeps its partials and arrival counters in a
-static device array instead of a caller workspace.  Two calls in a row (the
+``nsd_paged_attention_noalloc`` keeps the partials of segments cut into
+several pieces (normalised O and log-sum-exp per slot) in a static device
+array instead of a caller workspace.  Two calls in a row (the
 second with fewer rows and shorter contexts, so it reuses what the first left
 in the array) must give the workspace entry point's results, within the
 path's tolerance (o 2e-3 abs + 1e-2 rel, LSE 1e-4), and match the oracle.
