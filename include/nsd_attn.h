@@ -45,7 +45,7 @@ extern "C" {
 #define NSD_COPY_ENGINE_DMA 0     /* hipMemcpyAsync per run (system DMA engines) */
 #define NSD_COPY_ENGINE_KERNEL 1  /* one gfx950 copy launch over every run */
 
-#define NSD_PLAN_HEADER_WORDS 20
+#define NSD_PLAN_HEADER_WORDS 24
 
 /* Library version (major*10000 + minor*100 + patch). */
 int nsd_version(void);
@@ -151,14 +151,21 @@ int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_
  *     a verify group (rows of speculative.py:75-89); each group is attended
  *     once per KV head with GQA-group x q_len query rows packed together;
  *     max_group_rows = 1 keeps every row its own group;
- *   - the (group, kv head, 16-token block) stream is cut into n_workers
- *     contiguous ranges of near-equal cost (blocks plus a fixed charge per
- *     range piece), one per workgroup; a (group, kv head) segment cut
- *     across ranges gets partials (normalised O in fp16, log2-sum-exp in fp32),
- *     merged in slot order by a second launch of the same call.
- * nsd_attn_plan_bound gives the plan size in int32 words for plans that fit
- * n_workers workers.  A plan may use more workers than asked (a worker
- * streams at most 4 pieces and 1024 blocks); when it does not fit `plan_capacity`,
+ *   - every (group, kv head) segment is cut into near-equal pieces of
+ *     consecutive 16-token blocks (at most 256 each), n_workers pieces in
+ *     all: each segment starts with the fewest pieces it needs and every
+ *     further piece goes to the segment whose pieces are the longest (while
+ *     pieces stay >= 4 blocks and <= 128 per segment), so no cut into as
+ *     many pieces has a shorter longest piece;
+ *   - one workgroup streams one piece; pieces are dealt longest first to
+ *     the eight XCDs (workgroup i runs on XCD i % 8) with near-equal blocks
+ *     and counts per XCD, each XCD's list longest first;
+ *   - a segment cut into several pieces gets partials (normalised O in
+ *     fp16, log2-sum-exp in fp32), merged in slot order by a second launch
+ *     of the same call.
+ * nsd_attn_plan_bound gives the plan size in int32 words for plans of
+ * n_workers pieces; when a plan needs more (segments longer than 256
+ * blocks need several pieces each) and does not fit `plan_capacity`,
  * nsd_attn_plan_build returns NSD_ERR_WORKSPACE and sets *plan_words to the
  * size needed, so the caller can retry.
  * nsd_attn_plan_build validates (1 <= seq_len <= bt_stride*block_size,
@@ -172,6 +179,22 @@ int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_lens, int64_t
                         int64_t bt_rows, int64_t bt_stride, int n_workers,
                         int max_group_rows, int32_t* plan, int64_t plan_capacity,
                         int64_t* plan_words, int64_t* workspace_bytes);
+/*
+ * nsd_attn_plan_build_claimed: nsd_attn_plan_build, with the workgroup
+ * slots of the device given (static_slots, e.g. nsd_attn_num_workers):
+ * when the plan has more pieces than slots, only the static_slots longest
+ * are bound to workgroups (and XCDs) ahead of the launch; the rest are
+ * claimed at run time, longest first, by the workgroups that start as
+ * slots free up, so a faster XCD takes more of them.  static_slots = 0
+ * binds every piece (nsd_attn_plan_build).  The workspace then holds a
+ * claim counter that must be zero before the first call (every call leaves
+ * it zero): allocate it zero-filled.
+ */
+int nsd_attn_plan_build_claimed(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                                int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                int64_t bt_rows, int64_t bt_stride, int n_workers, int static_slots,
+                                int max_group_rows, int32_t* plan, int64_t plan_capacity,
+                                int64_t* plan_words, int64_t* workspace_bytes);
 
 /*
  * Number of workers (workgroups) that fill the current device for a plan
@@ -188,8 +211,11 @@ int nsd_attn_num_workers(int max_rows, int* n_workers);
  * softmax-weighted sum of V (fp16 out, fp32 math).  If lse != NULL it also
  * writes ln(sum exp(score)) as fp32 [n_rows, Hq].
  * plan_host / plan_dev: the same plan words on the host and on the device.
- * workspace: device buffer of at least the bytes reported by the plan (the
- * partials of the segments cut across workgroups), 16-byte aligned.  Calls
+ * workspace: device buffer of at least the bytes reported by the plan (a
+ * 256-byte claim counter, then the partials of the segments cut into
+ * pieces), 16-byte aligned.  The counter must be zero before the first call
+ * with a plan that has claimed pieces (nsd_attn_plan_build_claimed); every
+ * call leaves it zero, so allocate the workspace zero-filled once.  Calls
  * that share a workspace must be ordered on one stream (never concurrent).
  * bt_rows / bt_stride: the block table's shape; the plan must have been
  * built for this row stride and at most this many rows.

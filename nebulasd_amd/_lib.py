@@ -19,7 +19,7 @@ NSD_ERR_WORKSPACE = 4
 STATUS_BAD_BLOCK = 1
 STATUS_BAD_SEQ = 2
 STATUS_BAD_POSITION = 4
-PLAN_HEADER_WORDS = 20
+PLAN_HEADER_WORDS = 24
 COPY_D2H = 0
 COPY_H2D = 1
 COPY_ENGINE_DMA = 0
@@ -29,7 +29,7 @@ COPY_ENGINE_KERNEL = 1
 PLAN_MAGIC, PLAN_VERSION, PLAN_ROWS, PLAN_GROUPS, PLAN_PIECES, PLAN_WORKERS, PLAN_COMBINES, \
     PLAN_SLOTS, PLAN_ROWS_MAX, PLAN_HQ, PLAN_HKV, PLAN_OFF_GROUPS, PLAN_SIZED_FOR, \
     PLAN_OFF_PIECES, PLAN_OFF_COMBINES, PLAN_WORDS, PLAN_PIECE_BLOCKS, PLAN_BT_ROWS, \
-    PLAN_BT_STRIDE, PLAN_MAX_BLOCKS = range(20)
+    PLAN_BT_STRIDE, PLAN_MAX_BLOCKS, PLAN_STATIC, PLAN_CLAIMED = range(22)
 
 _I32P = POINTER(c_int32)
 
@@ -58,6 +58,9 @@ SIGNATURES = {
     "nsd_attn_plan_bound": (c_int64, [c_int64, c_int, c_int]),
     "nsd_attn_plan_build": (
         c_int, [_I32P, _I32P, c_int64, c_int, c_int, c_int, c_int, c_int64, c_int64, c_int, c_int,
+                _I32P, c_int64, POINTER(c_int64), POINTER(c_int64)]),
+    "nsd_attn_plan_build_claimed": (
+        c_int, [_I32P, _I32P, c_int64, c_int, c_int, c_int, c_int, c_int64, c_int64, c_int, c_int, c_int,
                 _I32P, c_int64, POINTER(c_int64), POINTER(c_int64)]),
     "nsd_attn_num_workers": (c_int, [c_int, POINTER(c_int)]),
     "nsd_paged_attention": (

@@ -92,6 +92,10 @@ struct AttnArgs {
   f16* part_o;             // [slots, rows_max, D]  normalised O
   float* part_lse;         // [slots, rows_max]  (log2 domain)
   const int32_t* combines; // plan: combine records of the segments cut into pieces
+  int32_t* claim;          // claim counter of the claimed records (zero between calls)
+  int n_static;            // workgroups below this stream the record of their index
+  int n_claimed;           // records after those, claimed in order by the later workgroups
+  int n_claim_wgs;         // the later workgroups (each claims once)
   int32_t* status;
   int64_t num_blocks;
   int64_t blk_stride;      // elements per cache block: L*Hkv*16*128
@@ -209,7 +213,23 @@ void paged_attn_kernel(AttnArgs a) {
   const lds_char* lds = lds_all + wave * kWaveLds;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
-  const int32_t* rec = a.pieces + (int64_t)blockIdx.x * kPieceWords;
+  int rec_idx = blockIdx.x;
+  if (rec_idx >= a.n_static) {
+    // claim the next record: one device-scope add per workgroup; the last
+    // workgroup to claim (every later workgroup claims exactly once) sets
+    // the counter back to zero for the next call
+    __shared__ int s_ticket;
+    if (threadIdx.x == 0) {
+      const int t = __hip_atomic_fetch_add(a.claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t == a.n_claim_wgs - 1) __hip_atomic_store(a.claim, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_ticket = t;
+    }
+    __syncthreads();
+    const int t = s_ticket;
+    if (t >= a.n_claimed) return;
+    rec_idx = a.n_static + t;
+  }
+  const int32_t* rec = a.pieces + (int64_t)rec_idx * kPieceWords;
   const int q_len = rec[kPieceQLen];
   if (q_len == 0) return;  // an empty record
   const int head = rec[kPieceHead], blk0 = rec[kPieceBlkBegin];
@@ -455,10 +475,10 @@ static __device__ __align__(256) char scratch[NSD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
-// Bytes of the partials a plan needs: normalised O (fp16) and log2-sum-exp
-// (fp32) per partial slot and row, rounded up to 256 bytes.
+// Workspace bytes a plan needs: the claim counter (when it has claimed
+// records) and the partials.
 int64_t plan_partial_bytes(const int32_t* plan_host) {
-  return ((int64_t)plan_host[kPlanSlots] * plan_host[kPlanRowsMax] * (int64_t)(D * 2 + 4) + 255) / 256 * 256;
+  return plan_workspace_bytes(plan_host[kPlanSlots], plan_host[kPlanRowsMax]);
 }
 
 // Shared body of the two attention entry points: `part` holds the partials
@@ -495,7 +515,10 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
     return fail(NSD_ERR_INVALID, "paged_attention: q/o/caches must be 16-byte aligned");
   const int nt = (rows_max + 15) / 16;
   const int64_t n_slots = plan_host[kPlanSlots];
-  if (rows_max < 1 || rows_max > kMaxGroupRows || grid % kXcds != 0 || plan_host[kPlanPieces] != grid ||
+  const int n_static = plan_host[kPlanStatic], n_claimed = plan_host[kPlanClaimed];
+  const int n_records = plan_host[kPlanPieces];
+  if (rows_max < 1 || rows_max > kMaxGroupRows || n_static < 0 || n_static % kXcds != 0 || n_claimed < 0 ||
+      n_records != n_static + n_claimed || grid < n_records || (n_claimed == 0 && grid != n_static) ||
       plan_host[kPlanMaxBlocks] < 1 || plan_host[kPlanMaxBlocks] > kMaxPieceBlocks || n_slots < 0 ||
       n_combine < 0)
     return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan header");
@@ -509,7 +532,7 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
   // against the buffers it will touch
   const int gqa = num_q_heads / num_kv_heads;
   const int32_t* pr = plan_host + plan_host[kPlanOffPieces];
-  for (int i = 0; i < grid; ++i) {
+  for (int i = 0; i < n_records; ++i) {
     const int32_t* r = pr + kPieceWords * i;
     if (r[kPieceQLen] == 0) continue;  // an empty record: its workgroup exits at once
     const int nb = r[kPieceBlkEnd] - r[kPieceBlkBegin];
@@ -536,7 +559,7 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
       return fail(NSD_ERR_INVALID, "paged_attention: corrupt plan (combine %d)", c);
   }
   const int64_t part_bytes = plan_partial_bytes(plan_host);
-  if (n_combine > 0 && (part == nullptr || part_capacity < part_bytes || !aligned16(part)))
+  if ((n_combine > 0 || n_claimed > 0) && (part == nullptr || part_capacity < part_bytes || !aligned16(part)))
     return fail(NSD_ERR_WORKSPACE,
                 "paged_attention: workspace holds %lld partial bytes, the plan needs %lld",
                 (long long)part_capacity, (long long)part_bytes);
@@ -550,8 +573,13 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
   args.bt = block_table;
   args.bt_stride = bt_stride;
   args.pieces = plan_dev + plan_host[kPlanOffPieces];
-  args.part_o = static_cast<f16*>(part);
-  args.part_lse = reinterpret_cast<float*>(static_cast<f16*>(part) + n_slots * rows_max * D);
+  char* ws = static_cast<char*>(part);
+  args.claim = n_claimed > 0 ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  args.n_static = n_static;
+  args.n_claimed = n_claimed;
+  args.n_claim_wgs = grid - n_static;
+  args.part_o = reinterpret_cast<f16*>(ws + kClaimBytes);
+  args.part_lse = reinterpret_cast<float*>(args.part_o + n_slots * rows_max * D);
   args.combines = plan_dev + plan_host[kPlanOffCombines];
   args.status = status;
   args.num_blocks = num_blocks;

@@ -41,6 +41,9 @@ enum PlanHeader {
   kPlanBtRows,         // block-table rows every piece's seq_id was checked against
   kPlanBtStride,       // block-table row length every piece's block range was checked against
   kPlanMaxBlocks,      // most 16-token blocks in one piece
+  kPlanStatic,         // workgroups 0 .. kPlanStatic-1 stream records of the same index
+  kPlanClaimed,        // records kPlanStatic .. +kPlanClaimed-1, claimed at run time by the
+                       // later workgroups in order (kPlanWorkers - kPlanStatic of them)
 };
 static_assert(kPlanMaxBlocks < NSD_PLAN_HEADER_WORDS, "plan header size");
 
@@ -66,7 +69,7 @@ enum PieceField {
 enum CombineField { kCombHead = 0, kCombFirst, kCombSlots, kCombRowStart, kCombQLen };
 
 constexpr int32_t kPlanMagicValue = 0x4E534450;
-constexpr int32_t kPlanVersionValue = 8;
+constexpr int32_t kPlanVersionValue = 9;
 constexpr int kHeadDim = 128;
 constexpr int kBlockTokens = 16;
 constexpr int kMaxGroupRows = 48;       // query rows of one segment: three 16-row tiles in one wave
@@ -74,5 +77,14 @@ constexpr int kMaxSlotsPerSegment = 128;
 constexpr int kMaxPieceBlocks = 256;    // blocks of one piece (four waves, one block id per lane)
 constexpr int kMinPieceBlocks = 4;
 constexpr int kXcds = 8;                // workgroup i of a launch runs on XCD i % 8
+
+// Attention workspace: the claim counter of plans with claimed records
+// (zero between calls; its 256 bytes are reserved in every layout, so no
+// other plan's partials land there), then the partials of the split
+// segments, normalised O (fp16) and log2-sum-exp (fp32) per slot and row.
+constexpr int64_t kClaimBytes = 256;
+inline int64_t plan_workspace_bytes(int64_t n_slots, int64_t rows_max) {
+  return kClaimBytes + (n_slots * rows_max * (int64_t)(kHeadDim * 2 + 4) + 255) / 256 * 256;
+}
 
 }  // namespace nsd

@@ -38,10 +38,11 @@ static int64_t round_up8(int64_t x) { return (x + 7) / 8 * 8; }
 extern "C" int64_t nsd_attn_plan_bound(int64_t n_rows, int num_kv_heads, int n_workers) {
   if (n_rows < 0 || num_kv_heads <= 0 || n_workers <= 0) return -1;
   const int64_t segs = n_rows * num_kv_heads;
-  // pieces: at most n_workers + segs for the chosen piece size (each segment
-  // adds at most one short piece), plus the empty records that even out the
-  // XCD lists; a plan that needs more reports its size and the caller retries
-  const int64_t pieces = round_up8((int64_t)n_workers + segs) + kXcds * kMaxSlotsPerSegment;
+  // pieces: n_workers, or one per segment where there are more segments,
+  // plus the empty records that even out the XCD lists; a plan that needs
+  // more (segments longer than 256 blocks each) reports its size and the
+  // caller retries
+  const int64_t pieces = round_up8(std::max<int64_t>(n_workers, segs)) + kXcds * kMaxSlotsPerSegment;
   return NSD_PLAN_HEADER_WORDS + 4 * n_rows + kPieceWords * pieces + kPieceWords * segs;
 }
 
@@ -50,6 +51,16 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
                                    int64_t bt_rows, int64_t bt_stride, int n_workers,
                                    int max_group_rows, int32_t* plan, int64_t plan_capacity,
                                    int64_t* plan_words, int64_t* workspace_bytes) {
+  return nsd_attn_plan_build_claimed(seq_ids, seq_lens, n_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+                                     bt_rows, bt_stride, n_workers, 0, max_group_rows, plan, plan_capacity,
+                                     plan_words, workspace_bytes);
+}
+
+extern "C" int nsd_attn_plan_build_claimed(const int32_t* seq_ids, const int32_t* seq_lens, int64_t n_rows,
+                                           int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                           int64_t bt_rows, int64_t bt_stride, int n_workers, int static_slots,
+                                           int max_group_rows, int32_t* plan, int64_t plan_capacity,
+                                           int64_t* plan_words, int64_t* workspace_bytes) {
   if (n_rows < 0) return fail(NSD_ERR_INVALID, "plan: n_rows=%lld < 0", (long long)n_rows);
   if (n_rows > 0 && (seq_ids == nullptr || seq_lens == nullptr))
     return fail(NSD_ERR_INVALID, "plan: null seq_ids/seq_lens");
@@ -62,6 +73,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   if (block_size != kBlockTokens)
     return fail(NSD_ERR_UNSUPPORTED, "plan: block_size=%d (only 16)", block_size);
   if (n_workers <= 0) return fail(NSD_ERR_INVALID, "plan: n_workers=%d", n_workers);
+  if (static_slots < 0) return fail(NSD_ERR_INVALID, "plan: static_slots=%d", static_slots);
   if (bt_rows <= 0 || bt_stride <= 0)
     return fail(NSD_ERR_INVALID, "plan: block table shape [%lld, %lld]", (long long)bt_rows,
                 (long long)bt_stride);
@@ -161,10 +173,17 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
     const auto bx = piece_blocks(x.first, x.second), by = piece_blocks(y.first, y.second);
     return bx.second - bx.first > by.second - by.first;
   });
-  const size_t cap = (size_t)((n_pieces + kXcds - 1) / kXcds);
+  //    With static_slots > 0 and more pieces than that, only the
+  //    static_slots (rounded down to a multiple of 8) longest go to the XCD
+  //    lists; the rest, longest first, are claimed at run time by the
+  //    workgroups that start as slots free up, whichever XCD they run on.
+  const int64_t n_static_pieces =
+      static_slots >= kXcds && n_pieces > static_slots ? static_slots / kXcds * kXcds : n_pieces;
+  const size_t cap = (size_t)((n_static_pieces + kXcds - 1) / kXcds);
   std::vector<std::vector<std::pair<int64_t, int64_t>>> lists(kXcds);
   std::vector<int64_t> load(kXcds, 0);
-  for (const auto& pc : all) {
+  for (int64_t i = 0; i < n_static_pieces; ++i) {
+    const auto& pc = all[i];
     int x = -1;
     for (int c = 0; c < kXcds; ++c)
       if (lists[c].size() < cap && (x < 0 || load[c] < load[x])) x = c;
@@ -172,6 +191,7 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
     load[x] += b.second - b.first;
     lists[x].push_back(pc);
   }
+  const std::vector<std::pair<int64_t, int64_t>> claimed(all.begin() + n_static_pieces, all.end());
   const size_t longest = n_pieces > 0 ? cap : 0;
   const int64_t target = n_pieces > 0 ? (total + n_pieces - 1) / n_pieces : 0;
 
@@ -190,11 +210,31 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   }
   const int64_t n_combines = (int64_t)combines.size() / kPieceWords;
 
-  // 6. records in dispatch order: position 8j + x holds the j-th piece of
-  //    XCD x's list, or an empty record where that list is shorter.
-  const int64_t grid = total > 0 ? kXcds * (int64_t)longest : 0;
-  std::vector<int32_t> records(kPieceWords * grid, 0);
+  // 6. records: first the static ones in dispatch order (position 8j + x
+  //    holds the j-th piece of XCD x's list, or an empty record where that
+  //    list is shorter), then the claimed ones in claim order.  Half again
+  //    as many workgroups as claimed records follow the static ones (each
+  //    claims one record or finds none left), so that an XCD whose slots
+  //    free up early can take more than its share.
+  const int64_t n_static = total > 0 ? kXcds * (int64_t)longest : 0;
+  const int64_t n_claimed = (int64_t)claimed.size();
+  const int64_t claim_wgs = round_up8((3 * n_claimed + 1) / 2);
+  const int64_t grid = n_static + claim_wgs;
+  const int64_t n_records = n_static + n_claimed;
+  std::vector<int32_t> records(kPieceWords * n_records, 0);
   int64_t max_blocks = 0;
+  auto fill = [&](int32_t* r, int64_t s, int64_t k) {
+    const auto b = piece_blocks(s, k);
+    const int32_t* g = &groups[4 * (s / num_kv_heads)];
+    const bool split = seg_pieces[s] > 1;
+    const int32_t rec[kPieceWords] = {
+        (int32_t)(s % num_kv_heads), (int32_t)b.first, (int32_t)b.second,
+        split ? (int32_t)(seg_slot[s] + k) : -1, g[0], g[1], g[2], g[3],
+        split ? (int32_t)seg_comb[s] : -1, split ? (int32_t)seg_slot[s] : 0,
+        split ? (int32_t)seg_pieces[s] : 0, (int32_t)s};
+    std::copy(rec, rec + kPieceWords, r);
+    max_blocks = std::max(max_blocks, b.second - b.first);
+  };
   for (int64_t j = 0; j < (int64_t)longest; ++j) {
     for (int x = 0; x < kXcds; ++x) {
       int32_t* r = &records[kPieceWords * (kXcds * j + x)];
@@ -204,20 +244,11 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
         r[kPieceSeg] = -1;
         continue;
       }
-      const int64_t s = lists[x][j].first, k = lists[x][j].second;
-      const auto b = piece_blocks(s, k);
-      const int32_t* g = &groups[4 * (s / num_kv_heads)];
-      const bool split = seg_pieces[s] > 1;
-      const int32_t rec[kPieceWords] = {
-          (int32_t)(s % num_kv_heads), (int32_t)b.first, (int32_t)b.second,
-          split ? (int32_t)(seg_slot[s] + k) : -1, g[0], g[1], g[2], g[3],
-          split ? (int32_t)seg_comb[s] : -1, split ? (int32_t)seg_slot[s] : 0,
-          split ? (int32_t)seg_pieces[s] : 0, (int32_t)s};
-      std::copy(rec, rec + kPieceWords, r);
-      max_blocks = std::max(max_blocks, b.second - b.first);
+      fill(r, lists[x][j].first, lists[x][j].second);
     }
   }
-  const int64_t n_records = grid;
+  for (int64_t i = 0; i < n_claimed; ++i)
+    fill(&records[kPieceWords * (n_static + i)], claimed[i].first, claimed[i].second);
 
   const int64_t off_groups = NSD_PLAN_HEADER_WORDS;
   const int64_t off_pieces = off_groups + 4 * n_groups;
@@ -253,13 +284,13 @@ extern "C" int nsd_attn_plan_build(const int32_t* seq_ids, const int32_t* seq_le
   h[kPlanBtRows] = (int32_t)std::min<int64_t>(bt_rows, INT32_MAX);
   h[kPlanBtStride] = (int32_t)std::min<int64_t>(bt_stride, INT32_MAX);
   h[kPlanMaxBlocks] = (int32_t)max_blocks;
+  h[kPlanStatic] = (int32_t)n_static;
+  h[kPlanClaimed] = (int32_t)n_claimed;
   std::copy(groups.begin(), groups.end(), h + off_groups);
   std::copy(records.begin(), records.end(), h + off_pieces);
   std::copy(combines.begin(), combines.end(), h + off_combines);
 
   *plan_words = words;
-  // partial O (fp16) and log-sum-exp (fp32) per slot and row
-  const int64_t part_bytes = (n_slots * rows_max * (int64_t)(kHeadDim * 2 + 4) + 255) / 256 * 256;
-  *workspace_bytes = n_combines > 0 ? part_bytes : 0;
+  *workspace_bytes = n_combines > 0 || n_claimed > 0 ? plan_workspace_bytes(n_slots, rows_max) : 0;
   return NSD_OK;
 }

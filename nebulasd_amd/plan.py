@@ -40,13 +40,15 @@ def num_workers(max_rows: int, device_index: int | None = None) -> int:
     return _workers_cache[key]
 
 
-# Pieces the planner cuts per workgroup slot: more, shorter pieces even out
-# the end of a launch; fewer, longer ones write fewer partials and start and
-# merge fewer pieces.  With one per slot every piece starts at once.
-# Measured (graph-timed layer calls, one box): verify 35.6 / 36.9 / 38.0 /
-# 42.5 us at 1 / 1.5 / 2 / 3 per slot, ragged verify 115.4 / 116.6 / 118.5 /
-# 121.6, decode 60.0 / 62.3 / 59.9 / 59.3 (520-byte partials).
-PIECES_PER_SLOT = {1: 2.0, 2: 1.0, 3: 1.0}
+# Pieces the planner cuts per workgroup slot.  One per slot binds every
+# piece to a workgroup and starts them all at once; more make the slots'
+# worth of longest pieces bound and the rest claimed at run time by the
+# workgroups that start as slots free up (a faster XCD takes more of them),
+# at the price of more pieces to start, merge and combine.  Measured
+# (graph-timed layer calls, one box, one run): verify 36.3 / 40.1 / 39.8 us
+# at 1 / 1.5 / 2 per slot, decode 63.2 / 64.0 / 62.8, ragged verify
+# (three 16-row tiles) 115.3 / 114.3 / 115.2.
+PIECES_PER_SLOT = {1: 2.0, 2: 1.0, 3: 1.5}
 
 
 def pieces_for(slots: int, max_rows: int) -> int:
@@ -59,8 +61,9 @@ def pieces_for(slots: int, max_rows: int) -> int:
 
 def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
                block_size: int, bt_rows: int, bt_stride: int, n_workers: int,
-               max_group_rows: int = 0) -> tuple[np.ndarray, int]:
-    """Run the native planner on host lists; returns (plan words int32, workspace bytes)."""
+               max_group_rows: int = 0, static_slots: int = 0) -> tuple[np.ndarray, int]:
+    """Run the native planner on host lists; returns (plan words int32, workspace bytes).
+    ``static_slots`` > 0: pieces beyond that many are claimed at run time."""
     sid = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int32))
     sl = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.int32))
     if sid.shape != sl.shape or sid.ndim != 1:
@@ -75,10 +78,10 @@ def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim:
         buf = np.zeros(cap, dtype=np.int32)
         words = ctypes.c_int64(0)
         ws = ctypes.c_int64(0)
-        rc = lib.nsd_attn_plan_build(
+        rc = lib.nsd_attn_plan_build_claimed(
             sid.ctypes.data_as(i32p), sl.ctypes.data_as(i32p), len(sid), num_q_heads,
-            num_kv_heads, head_dim, block_size, bt_rows, bt_stride, n_workers, max_group_rows,
-            buf.ctypes.data_as(i32p), cap, ctypes.byref(words), ctypes.byref(ws))
+            num_kv_heads, head_dim, block_size, bt_rows, bt_stride, n_workers, static_slots,
+            max_group_rows, buf.ctypes.data_as(i32p), cap, ctypes.byref(words), ctypes.byref(ws))
         if rc == _lib.NSD_ERR_WORKSPACE and words.value > cap:
             cap = words.value
             continue
@@ -90,9 +93,10 @@ def plan_words(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head_dim:
 def decode_plan(words: np.ndarray) -> dict:
     """Split plan words into named numpy views (for inspection and tests).
 
-    ``records`` holds one piece per workgroup in dispatch order (record i runs
-    on XCD i % 8; records with q_len 0 are empty); ``pieces`` lists the
-    non-empty ones in that order.
+    ``records`` holds the pieces: the first ``static`` in dispatch order
+    (record i runs on workgroup i, XCD i % 8; records with q_len 0 are
+    empty), then ``claimed`` more in the order the later workgroups claim
+    them; ``pieces`` lists the non-empty ones in that order.
     """
     h = words[:_lib.PLAN_HEADER_WORDS]
     n_groups, n_records = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_PIECES])
@@ -112,6 +116,8 @@ def decode_plan(words: np.ndarray) -> dict:
         "bt_rows": int(h[_lib.PLAN_BT_ROWS]),
         "bt_stride": int(h[_lib.PLAN_BT_STRIDE]),
         "max_blocks": int(h[_lib.PLAN_MAX_BLOCKS]),
+        "static": int(h[_lib.PLAN_STATIC]),
+        "claimed": int(h[_lib.PLAN_CLAIMED]),
         "groups": words[og:og + 4 * n_groups].reshape(n_groups, 4),
         "records": records,
         "pieces": records[used],
@@ -165,25 +171,28 @@ def build_attn_plan(seq_ids, seq_lens, num_q_heads: int, num_kv_heads: int, head
     device = torch.device(device)
     gqa = num_q_heads // num_kv_heads
     sized = n_workers is None
+    slots = 0
     if sized:
         # size the pieces for the row-tile count the grouping will produce
         guess = min(MAX_GROUP_ROWS, gqa * max(1, (max_group_rows or MAX_GROUP_ROWS) // gqa))
-        n_workers = pieces_for(num_workers(guess, device.index), guess)
+        slots = num_workers(guess, device.index)
+        n_workers = pieces_for(slots, guess)
     words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim, block_size,
-                           bt_rows, bt_stride, n_workers, max_group_rows)
+                           bt_rows, bt_stride, n_workers, max_group_rows, slots)
     rows_max = int(words[_lib.PLAN_ROWS_MAX])
     if sized and rows_max > 0 and n_workers != pieces_for(num_workers(rows_max, device.index), rows_max):
+        slots = num_workers(rows_max, device.index)
         words, ws = plan_words(seq_ids, seq_lens, num_q_heads, num_kv_heads, head_dim,
-                               block_size, bt_rows, bt_stride,
-                               pieces_for(num_workers(rows_max, device.index), rows_max), max_group_rows)
+                               block_size, bt_rows, bt_stride, pieces_for(slots, rows_max), max_group_rows,
+                               slots)
     # pinned and non-blocking: the upload does not wait for the stream
     # (the caching host allocator keeps the pinned block until the copy ran)
     src = torch.from_numpy(words)
     dev = (src.pin_memory().to(device, non_blocking=True) if device.type == "cuda"
            else src.to(device))
-    # the split segments' partials; every launch writes each slot before
-    # the merge reads it, so the buffer needs no initialisation
-    workspace = torch.empty(max(ws, 256), dtype=torch.uint8, device=device)
+    # the claim counter (zero before the first call; every call leaves it
+    # zero) and the split segments' partials
+    workspace = torch.zeros(max(ws, 256), dtype=torch.uint8, device=device)
     return AttnPlan(words, dev, workspace, ws, num_q_heads, num_kv_heads)
 
 

@@ -72,13 +72,15 @@ def test_error_paths_without_gpu(lib):
 MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, MAX_SLOTS, XCDS, MAX_GROUP_ROWS = 256, 4, 128, 8, 48
 
 
-def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096):
+def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096,
+          static_slots=0):
     from nebulasd_amd.plan import decode_plan, plan_words
 
     words, ws = plan_words(seq_ids, seq_lens, hq, hkv, 128, 16, bt_rows or (max(seq_ids) + 1),
-                           stride, workers, max_group_rows)
+                           stride, workers, max_group_rows, static_slots)
     p = decode_plan(words)
     p["requested_workers"] = workers
+    p["static_slots"] = static_slots
     return p, ws
 
 
@@ -95,15 +97,32 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
     # segment = (group, kv head); blocks of 16 tokens
     nblk = [(-(-(int(g[3]) + int(g[1])) // 16)) for g in groups for _ in range(hkv)]
     total = sum(nblk)
-    # one workgroup per record, a multiple of the XCD count; each XCD's
-    # records (i, i + 8, ...) are its pieces longest first, empty ones last,
-    # and the XCDs' lists differ in length by at most one
-    assert len(recs) == p["workers"] and p["workers"] % XCDS == 0
+    # static records: one workgroup each, a multiple of the XCD count; each
+    # XCD's records (i, i + 8, ...) are its pieces longest first, empty ones
+    # last, and the XCDs' lists differ in length by at most one.  Claimed
+    # records follow, longest first, none longer than a static one, with
+    # half again as many workgroups (rounded up to 8) to claim them.
+    n_static, n_claimed = p["static"], p["claimed"]
+    assert len(recs) == n_static + n_claimed and n_static % XCDS == 0
+    assert p["workers"] == n_static + -(-((3 * n_claimed + 1) // 2) // XCDS) * XCDS
+    claimed = recs[n_static:]
+    assert (claimed[:, 5] > 0).all()
+    csizes = (claimed[:, 2] - claimed[:, 1]).tolist()
+    assert csizes == sorted(csizes, reverse=True)
+    if n_claimed:
+        assert n_static == p["static_slots"] // XCDS * XCDS
+        assert min(int(r[2] - r[1]) for r in recs[:n_static] if r[5] > 0) >= csizes[0]
     load, n_live_of = [0] * XCDS, []
     covered = [np.zeros(n, int) for n in nblk]
     pieces_of = {}
+    for rec in claimed:
+        h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, seg = (int(v) for v in rec)
+        assert h == seg % hkv and (row_start, q_len, sid, ctx) == tuple(int(v) for v in groups[seg // hkv])
+        assert 0 <= bb < be <= nblk[seg] and be - bb <= MAX_PIECE_BLOCKS
+        covered[seg][bb:be] += 1
+        pieces_of.setdefault(seg, []).append((bb, be, slot, comb, cfirst, cslots))
     for x in range(XCDS):
-        mine = recs[x::XCDS]
+        mine = recs[:n_static][x::XCDS]
         live = mine[:, 5] > 0
         n_live = int(live.sum())
         n_live_of.append(n_live)
@@ -122,7 +141,7 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
             assert int(rec[5]) == 0 and int(rec[3]) == -1
     assert all((c == 1).all() for c in covered)
     if nblk:
-        assert max(n_live_of) - min(n_live_of) <= 1 and max(n_live_of) == p["workers"] // XCDS
+        assert max(n_live_of) - min(n_live_of) <= 1 and max(n_live_of) == n_static // XCDS
         assert max(load) - min(load) <= 2 * p["max_blocks"]
     assert p["max_blocks"] == max((int(r[2] - r[1]) for r in p["pieces"]), default=0)
     # pieces per segment: at least ceil(blocks / 256); in all, as many as the
@@ -202,8 +221,9 @@ def test_plan_invariants_random(lib, seed):
     for hq, hkv in ((32, 8), (16, 8), (8, 8)):
         p, ws = _plan(seq_ids, seq_lens, hq, hkv, workers, bt_rows=100)
         check_plan_invariants(p, seq_ids, seq_lens, hkv, hq // hkv)
-        # partials: fp16 O (128 x 2 bytes) + fp32 lse per slot row
-        part = -(-p["slots"] * p["rows_max"] * (128 * 2 + 4) // 256) * 256
+        # 256 bytes for the claim counter, then the partials: fp16 O (128 x 2
+        # bytes) + fp32 lse per slot row, rounded up to 256 bytes
+        part = 256 + -(-p["slots"] * p["rows_max"] * (128 * 2 + 4) // 256) * 256
         assert ws == (part if len(p["combines"]) else 0)
 
 
@@ -291,6 +311,25 @@ def test_plan_respects_kernel_limits(lib):
     assert len(p["pieces"]) == 8 * 16
 
 
+@pytest.mark.parametrize("slots", [64, 100, 512])
+def test_plan_claimed_records(lib, slots):
+    """More pieces than workgroup slots: the slots' worth of longest pieces
+    are bound to workgroups, the rest claimed at run time, longest first."""
+    rng = np.random.default_rng(slots)
+    ctx = rng.integers(256, 4097, 16)
+    sid = [i for i in range(16) for _ in range(9)]
+    sl = [int(c) + 1 + k for c in ctx for k in range(9)]
+    p, ws = _plan(sid, sl, workers=3 * slots // 2, bt_rows=16, static_slots=slots)
+    check_plan_invariants(p, sid, sl, 8, 4)
+    n_pieces = max(3 * slots // 2, 16 * 8)  # at least one piece per (request, kv head)
+    assert len(p["pieces"]) == n_pieces and p["claimed"] == n_pieces - slots // 8 * 8 and ws > 0
+    # nothing to claim when every piece has a slot
+    p, _ = _plan(sid, sl, workers=slots, bt_rows=16, static_slots=slots)
+    check_plan_invariants(p, sid, sl, 8, 4)
+    if slots >= 16 * 8:
+        assert p["claimed"] == 0 and p["workers"] == p["static"]
+
+
 def test_plan_xcd_lists_balance(lib):
     # the verify shape: 16 requests x 8 kv heads over 8 XCDs, equal blocks per XCD
     rng = np.random.default_rng(3)
@@ -344,6 +383,8 @@ def test_attention_rejects_corrupt_plans(lib):
         (corrupt(_lib.PLAN_MAX_BLOCKS, 257), "header"),
         (corrupt(_lib.PLAN_PIECES, int(h[_lib.PLAN_PIECES]) + 1), "header"),
         (corrupt(_lib.PLAN_WORKERS, int(h[_lib.PLAN_WORKERS]) + 8), "header"),
+        (corrupt(_lib.PLAN_STATIC, int(h[_lib.PLAN_STATIC]) - 3), "header"),    # not whole XCD rows
+        (corrupt(_lib.PLAN_CLAIMED, 5), "header"),                              # records != static + claimed
         (corrupt(op + 2, words[op + 1] + 257), "piece 0"),                      # > 256 blocks
         (corrupt(op + 6, 2), "piece 0"),                                        # seq_id past the table
         (corrupt(op + 2, 4096 * 2), "piece 0"),                                 # past the block table row
