@@ -15,15 +15,18 @@
 // 4g .. 4g+3, so the S^T of a block is already the P^T operand of its PV
 // product, and a row's online-softmax state lives in one lane column.
 //
-// Work split.  The host planner cuts every segment into pieces of a few
-// 16-token blocks; one workgroup of ONE wave streams one piece, and the
-// hardware hands pieces to CU slots as slots free up (longest pieces first,
-// each XCD's share in its own interleaved list).  The wave brings each
-// block's K tile and V tile (4 KB each) straight from HBM into its own LDS
-// double buffer with global_load_lds_dwordx4 and computes the previous block
-// while the next one is in flight: no wave waits for another, so ten waves
-// per CU keep 80 KB of reads in flight between them.  The block ids are read
-// from the block table once per piece, one lane per block.
+// Work split.  The host planner cuts every segment into near-equal pieces
+// of 16-token blocks; one workgroup of four waves streams one piece.  The
+// pieces that fit the device's workgroup slots are bound to workgroups
+// ahead of the launch (workgroup i runs on XCD i % 8; each XCD's list
+// longest first); any more are claimed at run time, one device-scope add
+// per later workgroup, so an XCD whose slots free up early takes more.
+// Wave w streams blocks w, w + 4, ... of the piece: it brings each block's
+// K tile and V tile (4 KB each) straight from HBM into its own LDS double
+// buffer with global_load_lds_dwordx4 and computes the previous block while
+// the next one is in flight, with no barrier in the loop; the four waves'
+// softmax states are merged at the end of the piece.  The block ids are
+// read from the block table once per piece, one lane per block.
 //
 // Ring rows are XOR-swizzled per 16-byte chunk (swz_k, swz_v) by permuting
 // which source chunk each lane's DMA fetches, so the score MFMA's K reads
@@ -34,11 +37,12 @@
 // only when a wave-wide vote finds a score 2^8 above it (exact after the
 // final normalisation).
 //
-// Deterministic by construction: a piece's blocks are summed in order by one
-// wave, segments cut into several pieces write partials (normalised O in
-// fp16, log2-sum-exp in fp32) to fixed slots, and a second, small launch
-// merges each such segment's slots in slot order (the reference's phase 2).
-// Identical inputs give identical bits whichever CU runs which piece.
+// Deterministic by construction: which blocks a piece covers, which wave
+// sums which block and the merge order are fixed by the plan; segments cut
+// into several pieces write partials (normalised O in fp16, log2-sum-exp in
+// fp32) to fixed slots, and a second, small launch merges each such
+// segment's slots in slot order (the reference's phase 2).  Identical inputs
+// give identical bits whichever CU or workgroup runs which piece.
 //
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB
