@@ -1512,6 +1512,19 @@ def main():
     del w
     torch.cuda.empty_cache()
     secondary = {}
+    # the other attention workloads first, right after the headline: the
+    # path's own legs, measured before the longer widening legs load the GPU
+    for name in filter(None, args.secondary.split(",")):
+        r2, w2 = measure(name, args.seed, args.steps, args.warmup)
+        if args.probes:
+            with_gather_floor(r2, w2, args.steps, args.warmup)
+        print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
+              f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+        if args.cpu_baseline_seconds > 0:
+            r2["cpu_baseline"] = cpu_baseline(w2, args.other_cpu_seconds)
+        secondary[name] = r2
+        del w2
+        torch.cuda.empty_cache()
     for name in filter(None, args.prefill.split(",")):
         r2 = measure_prefill(name, args.seed, args.steps, args.warmup, args.other_cpu_seconds
                              if args.cpu_baseline_seconds > 0 else 0)
@@ -1566,17 +1579,6 @@ def main():
             f"{r2['swap_128_scattered_blocks']['in']['dma_gbps']:.1f} / "
             f"{r2['swap_128_scattered_blocks']['in']['kernel_gbps']:.1f}", file=sys.stderr, flush=True)
         secondary[r2["workload"]] = r2
-    for name in filter(None, args.secondary.split(",")):
-        r2, w2 = measure(name, args.seed, args.steps, args.warmup)
-        if args.probes:
-            with_gather_floor(r2, w2, args.steps, args.warmup)
-        print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
-              f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
-        if args.cpu_baseline_seconds > 0:
-            r2["cpu_baseline"] = cpu_baseline(w2, args.other_cpu_seconds)
-        secondary[name] = r2
-        del w2
-        torch.cuda.empty_cache()
     if args.spec_loop:
         r2 = measure_spec_loop(args.seed, args.steps, args.other_cpu_seconds if args.cpu_baseline_seconds > 0 else 0)
         print("# speculative loop shapes: " + "; ".join(
