@@ -13,6 +13,7 @@ import torch
 
 import oracle
 from helpers import ATOL_LSE, ATOL_O, RTOL_O, assert_close, compact_cache
+from nebulasd_amd import _lib
 from nebulasd_amd.config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from nebulasd_amd.infer_state import build_infer_state, rope_cache
 from nebulasd_amd.kernels import paged_attention
@@ -197,11 +198,16 @@ def test_attention_no_rows(gpu):
                     torch.empty_like(q))
 
 
-def test_attention_graph_replay_bit_identical(gpu):
+@pytest.mark.parametrize("q_len", [5, 1, 9], ids=["verify-bound", "decode-claimed", "q9-claimed"])
+def test_attention_graph_replay_bit_identical(gpu, q_len):
     """A HIP graph of attention calls over every layer replays to the eager
-    results bit for bit, replay after replay, with eager work in between."""
+    results bit for bit, replay after replay, with eager work in between.
+    Decode and 9-row groups cut more pieces than the device has workgroup
+    slots, so their later workgroups claim pieces from the workspace's
+    counter, which every call (replayed or eager) must leave at zero."""
+    print(f"graph replay, q_len {q_len}", flush=True)
     w = make_workload("target_verify", 9, device=gpu, pool_blocks=4096, num_layers=3,
-                      ctxs=[3000, 40, 1500, 700, 9], q_len=5)
+                      ctxs=[3000, 40, 1500, 700, 9], q_len=q_len)
     mc = ModelConfig(w.spec.model)
     ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
     cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)
@@ -217,7 +223,9 @@ def test_attention_graph_replay_bit_identical(gpu):
     calls()
     torch.cuda.synchronize()
     eager = [(o.clone(), l.clone()) for o, l in zip(outs, lses)]
-    assert int(st.attn_plan.host[6]) > 0, "expected split segments (the partial merge launch)"
+    assert int(st.attn_plan.host[_lib.PLAN_COMBINES]) > 0, "expected split segments (the partial merge launch)"
+    if q_len != 5:
+        assert int(st.attn_plan.host[_lib.PLAN_CLAIMED]) > 0, "expected claimed pieces"
     stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):

@@ -43,7 +43,10 @@ def noalloc_call(w, st, mc, layer, o, lse):
     dict(ctxs=[20000, 33, 9000, 1, 4000], q_len=5, seed=11),
     # the smaller second call: fewer rows, shorter contexts
     dict(ctxs=[700, 2500, 64], q_len=5, seed=12),
-], ids=["first-long", "second-smaller"])
+    # decode rows: more pieces than workgroup slots, the later ones claimed
+    # through the counter at the start of the static array
+    dict(ctxs=[20000, 33, 9000, 1, 4000], q_len=1, seed=13),
+], ids=["first-long", "second-smaller", "third-decode-claimed"])
 def test_noalloc_matches_workspace_entry(gpu, case):
     w = make_workload("target_verify", case["seed"], device=gpu, pool_blocks=4096, num_layers=2,
                       ctxs=case["ctxs"], q_len=case["q_len"])
@@ -62,6 +65,8 @@ def test_noalloc_matches_workspace_entry(gpu, case):
     torch.cuda.synchronize()
     if case["seed"] == 11:
         assert int(st.attn_plan.host[_lib.PLAN_COMBINES]) > 0, "expected split segments"
+    if case["seed"] == 13:
+        assert int(st.attn_plan.host[_lib.PLAN_CLAIMED]) > 0, "expected claimed pieces"
     e_o = assert_close(o2.float().cpu().numpy(), o1.float().cpu().numpy(), ATOL_O, RTOL_O,
                        "noalloc o vs workspace entry")
     e_l = assert_close(l2.cpu().numpy(), l1.cpu().numpy(), ATOL_LSE, 0.0,
