@@ -73,6 +73,10 @@ static_assert(kWaves * kMergeWave <= kLdsBytes, "merge fits in the buffer's LDS"
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLazyMax = 8.f;       // the running max moves only when exceeded by 2^8
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);  // s_waitcnt vmcnt(0), other counters open
+#ifndef NSD_ATTN_COMBINE_TABLE
+#define NSD_ATTN_COMBINE_TABLE 1
+#endif
+constexpr bool kUseCombineTable = NSD_ATTN_COMBINE_TABLE != 0;
 static_assert(kMaxGroupRows <= 48, "at most three 16-row tiles per wave");
 static_assert(kMaxPieceBlocks <= kWaves * kWave, "one block id per lane of its wave");
 
@@ -146,18 +150,16 @@ __device__ inline float rows_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Second launch: merge the partials of the segments cut into pieces.
-// Workgroup (c, g) merges rows 16g .. 16g+15 of combine record c; thread
-// (row, 8 dims), slots folded in slot order with a running max (online
-// log-sum-exp), eight slots' loads in flight at a time.  Same exp2-domain
-// combine as phase 2 of the reference (paged_attn.py:128-149).  The kernel
-// boundary orders it after every partial store of the attention launch.
-__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a, int row_groups) {
-  const int32_t* c = a.combines + kPieceWords * (blockIdx.x / row_groups);
-  const int n = 16 * (blockIdx.x % row_groups) + (threadIdx.x >> 4);
-  const int h = c[kCombHead], first = c[kCombFirst], n_slots = c[kCombSlots];
-  if (n >= c[kCombQLen] * a.gqa) return;
-  const int d8 = threadIdx.x & 15;
+// Second launch: merge the partials of the segments cut into pieces, the
+// same exp2-domain combine as phase 2 of the reference
+// (paged_attn.py:128-149).  The kernel boundary orders it after every partial
+// store of the attention launch.
+// Row n (of the segment's q_len x GQA rows), dims 8 d8 .. 8 d8 + 7, of a
+// split segment of kv head `head` whose partials sit in slots [first, first
+// + n_slots): the slots folded in slot order with a running max (online
+// log-sum-exp), eight slots' loads in flight at a time, and the row stored.
+__device__ inline void merge_row(const AttnArgs& a, int head, int first, int n_slots, int row_start, int n,
+                                 int d8) {
   const f16* po = a.part_o + ((int64_t)first * a.rows_max + n) * D + 8 * d8;
   const float* pl = a.part_lse + (int64_t)first * a.rows_max + n;
   const int64_t sstride = (int64_t)a.rows_max * D;  // elements between slots
@@ -194,12 +196,40 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a, int row_groups
   }
   const float inv = 1.f / W;
   const int qi = n / a.gqa, gh = n - qi * a.gqa;
-  const int64_t orow = (int64_t)(c[kCombRowStart] + qi) * a.hq + h * a.gqa + gh;
+  const int64_t orow = (int64_t)(row_start + qi) * a.hq + head * a.gqa + gh;
   f16x8 hv = {(f16)(acc0[0] * inv), (f16)(acc0[1] * inv), (f16)(acc0[2] * inv),
               (f16)(acc0[3] * inv), (f16)(acc1[0] * inv), (f16)(acc1[1] * inv),
               (f16)(acc1[2] * inv), (f16)(acc1[3] * inv)};
   *reinterpret_cast<f16x8*>(a.o + orow * D + 8 * d8) = hv;
   if (d8 == 0 && a.lse != nullptr) a.lse[orow] = (M + __log2f(W)) * kLn2;
+}
+
+// Workgroup (c, g) merges rows 16g .. 16g+15 of combine record c, one thread
+// per (row, 8 dims).
+__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a, int row_groups) {
+  const int32_t* c = a.combines + kPieceWords * (blockIdx.x / row_groups);
+  const int n = 16 * (blockIdx.x % row_groups) + (threadIdx.x >> 4);
+  if (n >= c[kCombQLen] * a.gqa) return;
+  merge_row(a, c[kCombHead], c[kCombFirst], c[kCombSlots], c[kCombRowStart], n, threadIdx.x & 15);
+}
+
+// The combine records of plans with at most kCombineTableMax of them, packed
+// into the launch's arguments (64 bits each: first slot 20, slots 8, kv head
+// 8, first row 20, q_len 8), so that a workgroup reads its record with the
+// arguments instead of one more dependent load.
+constexpr int kCombineTableMax = 448;
+struct CombineTable {
+  uint64_t e[kCombineTableMax];
+};
+
+// Workgroup (c, g) = (blockIdx.x, blockIdx.y): the entry's address depends on
+// the workgroup index alone, so it loads with the other arguments.
+__global__ __launch_bounds__(256) void combine_table_kernel(AttnArgs a, CombineTable tab) {
+  const uint64_t e = tab.e[blockIdx.x];
+  const int n = 16 * (int)blockIdx.y + (threadIdx.x >> 4);
+  if (n >= (int)(e >> 56) * a.gqa) return;
+  merge_row(a, (int)((e >> 28) & 0xff), (int)(e & 0xfffff), (int)((e >> 20) & 0xff), (int)((e >> 36) & 0xfffff), n,
+            threadIdx.x & 15);
 }
 
 // One workgroup streams one piece: blocks [blk_begin, blk_end) of a (group,
@@ -601,7 +631,23 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
                  : nt == 2 ? launch_nt<2>(args, grid, st)
                            : launch_nt<3>(args, grid, st);
   if (rc != NSD_OK || n_combine == 0) return rc;
-  hipLaunchKernelGGL(combine_kernel, dim3(n_combine * nt), dim3(256), 0, st, args, nt);
+  const int32_t* crec = plan_host + plan_host[kPlanOffCombines];
+  bool packed = kUseCombineTable && n_combine <= kCombineTableMax;
+  CombineTable tab;
+  for (int c = 0; packed && c < n_combine; ++c) {
+    const int32_t* r = crec + kPieceWords * c;
+    if (r[kCombFirst] >= (1 << 20) || r[kCombSlots] >= 256 || r[kCombHead] >= 256 || r[kCombRowStart] >= (1 << 20) ||
+        r[kCombQLen] >= 256) {
+      packed = false;
+      break;
+    }
+    tab.e[c] = (uint64_t)r[kCombFirst] | (uint64_t)r[kCombSlots] << 20 | (uint64_t)r[kCombHead] << 28 |
+               (uint64_t)r[kCombRowStart] << 36 | (uint64_t)r[kCombQLen] << 56;
+  }
+  if (packed)
+    hipLaunchKernelGGL(combine_table_kernel, dim3(n_combine, nt), dim3(256), 0, st, args, tab);
+  else
+    hipLaunchKernelGGL(combine_kernel, dim3(n_combine * nt), dim3(256), 0, st, args, nt);
   return launch_status("paged_attention: partial merge");
 }
 
