@@ -77,6 +77,10 @@ constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);  // s_waitcnt vmcnt(0), oth
 #define NSD_ATTN_COMBINE_TABLE 1
 #endif
 constexpr bool kUseCombineTable = NSD_ATTN_COMBINE_TABLE != 0;
+#ifndef NSD_ATTN_PIECE_TABLE
+#define NSD_ATTN_PIECE_TABLE 1
+#endif
+constexpr bool kUsePieceTable = NSD_ATTN_PIECE_TABLE != 0;
 static_assert(kMaxGroupRows <= 48, "at most three 16-row tiles per wave");
 static_assert(kMaxPieceBlocks <= kWaves * kWave, "one block id per lane of its wave");
 
@@ -104,6 +108,7 @@ struct AttnArgs {
   int n_static;            // workgroups below this stream the record of their index
   int n_claimed;           // records after those, claimed in order by the later workgroups
   int n_claim_wgs;         // the later workgroups (each claims once)
+  int piece_table;         // 1: the static pieces' block-table positions are in the PieceTable argument
   int32_t* status;
   int64_t num_blocks;
   int64_t blk_stride;      // elements per cache block: L*Hkv*16*128
@@ -237,9 +242,18 @@ __global__ __launch_bounds__(256) void combine_table_kernel(AttnArgs a, CombineT
 // Block j goes to wave j % 4, which streams its blocks through its own
 // double buffer and keeps its own softmax state; the four states are merged
 // in wave order at the end.
+// Block-table positions of the static pieces (32 bits each: seq_id 16, first
+// block 16), packed into the launch's arguments when there are at most
+// kPieceTableMax of them: a workgroup's block ids then load beside its
+// record instead of after it.
+constexpr int kPieceTableMax = 920;
+struct PieceTable {
+  uint32_t e[kPieceTableMax];
+};
+
 template <int NT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void paged_attn_kernel(AttnArgs a) {
+void paged_attn_kernel(AttnArgs a, PieceTable pt) {
   extern __shared__ __align__(16) char smem_raw[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -263,13 +277,33 @@ void paged_attn_kernel(AttnArgs a) {
     if (t >= a.n_claimed) return;
     rec_idx = a.n_static + t;
   }
-  const int32_t* rec = a.pieces + (int64_t)rec_idx * kPieceWords;
-  const int q_len = rec[kPieceQLen];
+  // a static workgroup with the table reads block ids right away (lanes past
+  // the piece read a clamped, in-row column and are discarded below)
+  const bool tabled = a.piece_table != 0 && (int)blockIdx.x < a.n_static;
+  int tab_id = 0;
+  if (tabled) {
+    const uint32_t e = pt.e[blockIdx.x];
+    int64_t col = (int64_t)(e >> 16) + wave + kWaves * lane;
+    col = col < a.bt_stride ? col : a.bt_stride - 1;
+    tab_id = a.bt[(int64_t)(e & 0xffffu) * a.bt_stride + col];
+  }
+  // the whole record in one round of scalar loads: the index is uniform and
+  // the plan is read-only to the kernel (constant address space)
+  using const_i32p = const __attribute__((address_space(4))) int32_t*;
+  const const_i32p rec = (const_i32p)(uintptr_t)(a.pieces + (int64_t)__builtin_amdgcn_readfirstlane(rec_idx) * kPieceWords);
+  int32_t rv[kPieceWords];
+#pragma unroll
+  for (int i = 0; i < kPieceWords; ++i) rv[i] = rec[i];
+  // every field is used before the empty-record test, so the loads go out
+  // together rather than the rest after that test
+  asm volatile("" ::"s"(rv[0]), "s"(rv[1]), "s"(rv[2]), "s"(rv[3]), "s"(rv[4]), "s"(rv[5]), "s"(rv[6]),
+               "s"(rv[7]), "s"(rv[8]), "s"(rv[9]), "s"(rv[10]), "s"(rv[11]));
+  const int q_len = rv[kPieceQLen];
   if (q_len == 0) return;  // an empty record
-  const int head = rec[kPieceHead], blk0 = rec[kPieceBlkBegin];
-  const int nb = rec[kPieceBlkEnd] - blk0;  // 1 .. kMaxPieceBlocks (host-checked)
+  const int head = rv[kPieceHead], blk0 = rv[kPieceBlkBegin];
+  const int nb = rv[kPieceBlkEnd] - blk0;  // 1 .. kMaxPieceBlocks (host-checked)
   const int my_n = nb > wave ? (nb - wave + kWaves - 1) / kWaves : 0;  // this wave's blocks
-  const int row_start = rec[kPieceRowStart], ctx = rec[kPieceCtx];
+  const int row_start = rv[kPieceRowStart], ctx = rv[kPieceCtx];
   const int lr = lane & 15;   // row of a 16-row tile (B/D column)
   const int lg = lane >> 4;   // k-group of the MFMA operands
   const int n_rows = q_len * a.gqa;
@@ -279,31 +313,12 @@ void paged_attn_kernel(AttnArgs a) {
   int64_t boff = 0;
   bool bad = false;
   if (lane < my_n) {
-    const int id = a.bt[(int64_t)rec[kPieceSeqId] * a.bt_stride + blk0 + wave + kWaves * lane];
+    const int id = tabled ? tab_id : a.bt[(int64_t)rv[kPieceSeqId] * a.bt_stride + blk0 + wave + kWaves * lane];
     bad = id < 0 || id >= a.num_blocks;
     boff = (int64_t)(bad ? 0 : id) * a.blk_stride + ((int64_t)a.layer * a.hkv + head) * BS * D;
   }
   const uint64_t bad_mask = __builtin_amdgcn_ballot_w64(bad);
   if (bad_mask != 0 && lane == 0) flag_status(a.status, NSD_STATUS_BAD_BLOCK);
-
-  // Query rows of each row tile as the B operand of the score MFMA (lane
-  // (lg, lr): dims 32kk + 8lg .. +7 of row lr); rows past the group read its
-  // row 0 and are never stored.
-  f16x8 qf[NT][4];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int n = 16 * t + lr;
-    const int nr = n < n_rows ? n : 0;
-    const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
-    const f16* qrow = a.q + ((int64_t)(row_start + qi) * a.hq + head * a.gqa + gh) * D;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *reinterpret_cast<const f16x8*>(qrow + 32 * kk + 8 * lg);
-  }
-  // ids and query rows complete here, before the buffer loads the compiler
-  // does not see are issued: the builtin tells the compiler they are done,
-  // so it inserts no wait for them inside the loop (which would drain the
-  // buffer loads too: vmcnt retires in order)
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
   // DMA sources: load c of a tile fills rows 4c .. 4c+3 (lane l: row 4c + l/16,
   // stored chunk l % 16), fetching the chunk the swizzle puts there.
@@ -328,6 +343,28 @@ void paged_attn_kernel(AttnArgs a) {
     for (int c = 0; c < 4; ++c) dma_load(slot + kTile + c * 1024, vb + vsrc[c]);
   };
 
+  // The first two blocks' loads go out before the query rows', so the rows
+  // arrive under the blocks' latency; then everything issued so far has
+  // landed (the builtin also tells the compiler its own loads are done, so
+  // it inserts no wait for them inside the loop, which would drain the
+  // buffer loads too: vmcnt retires in order).
+  if (my_n > 0) issue(0);
+  if (my_n > 1) issue(1);
+  // Query rows of each row tile as the B operand of the score MFMA (lane
+  // (lg, lr): dims 32kk + 8lg .. +7 of row lr); rows past the group read its
+  // row 0 and are never stored.
+  f16x8 qf[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = 16 * t + lr;
+    const int nr = n < n_rows ? n : 0;
+    const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
+    const f16* qrow = a.q + ((int64_t)(row_start + qi) * a.hq + head * a.gqa + gh) * D;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *reinterpret_cast<const f16x8*>(qrow + 32 * kk + 8 * lg);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
   // LDS read addresses (bytes within a slot): the score operand of k-step kk
   // (row lr, chunk 4kk + lg) and the transposing V read of dim tile mt (row
   // 4lg + lr/4, dims 16mt + 4(lr%4) .. +3).
@@ -351,13 +388,14 @@ void paged_attn_kernel(AttnArgs a) {
     for (int mt = 0; mt < 8; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  if (my_n > 0) issue(0);
   for (int jj = 0; jj < my_n; ++jj) {
-    if (jj + 1 < my_n) {
-      issue(jj + 1);
-      wait_vm<8>();  // this block landed; the next stays in flight
-    } else {
-      wait_vm<0>();
+    if (jj > 0) {  // blocks 0 and 1 are in; block jj + 1 goes into the slot block jj - 1 freed
+      if (jj + 1 < my_n) {
+        issue(jj + 1);
+        wait_vm<8>();  // this block landed; the next stays in flight
+      } else {
+        wait_vm<0>();
+      }
     }
     const lds_char* sl = lds + (jj & 1) * kSlot;
     const int blk = blk0 + wave + kWaves * jj;
@@ -416,7 +454,7 @@ void paged_attn_kernel(AttnArgs a) {
   // buffer's LDS: wave w then owns dim tiles 2w, 2w + 1 of every row, sums
   // the waves' accumulators for them in wave order, and stores them (the
   // output, or the segment's partial).  Wave 0 writes the rows' LSE.
-  const int slot = rec[kPieceSlot];
+  const int slot = rv[kPieceSlot];
   float* mrg = (float*)smem_raw;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -470,8 +508,8 @@ void paged_attn_kernel(AttnArgs a) {
 }
 
 template <int NT>
-int launch_nt(const AttnArgs& args, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(kThreads), kLdsBytes, stream, args);
+int launch_nt(const AttnArgs& args, const PieceTable& pt, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(kThreads), kLdsBytes, stream, args, pt);
   return launch_status("paged_attention");
 }
 
@@ -627,9 +665,22 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
   args.scale_log2 = softmax_scale * 1.4426950408889634f;
 
   hipStream_t st = as_stream(stream);
-  const int rc = nt == 1 ? launch_nt<1>(args, grid, st)
-                 : nt == 2 ? launch_nt<2>(args, grid, st)
-                           : launch_nt<3>(args, grid, st);
+  // the static pieces' block-table positions, when they fit the arguments
+  PieceTable pt;
+  args.piece_table = kUsePieceTable && n_static <= kPieceTableMax ? 1 : 0;
+  for (int i = 0; args.piece_table && i < n_static; ++i) {
+    const int32_t* r = pr + kPieceWords * i;
+    const bool live = r[kPieceQLen] != 0;
+    const int32_t sid = live ? r[kPieceSeqId] : 0, b0 = live ? r[kPieceBlkBegin] : 0;
+    if (sid >= (1 << 16) || b0 >= (1 << 16)) {
+      args.piece_table = 0;
+      break;
+    }
+    pt.e[i] = (uint32_t)sid | (uint32_t)b0 << 16;
+  }
+  const int rc = nt == 1 ? launch_nt<1>(args, pt, grid, st)
+                 : nt == 2 ? launch_nt<2>(args, pt, grid, st)
+                           : launch_nt<3>(args, pt, grid, st);
   if (rc != NSD_OK || n_combine == 0) return rc;
   const int32_t* crec = plan_host + plan_host[kPlanOffCombines];
   bool packed = kUseCombineTable && n_combine <= kCombineTableMax;
