@@ -1621,7 +1621,7 @@ def main():
             "unit": "GB/s",
             "frac": res["hbm_frac"],
             "traffic": traffic_from_profiles(args.workload),
-            "kernels": "paged_attn_kernel (+ combine_kernel for split segments), one layer call",
+            "kernels": "paged_attn_kernel (+ combine_table_kernel, the merge of split segments), one layer call",
         },
         "copy_probe_gbps": copy_gbps,
         "probes": _compact_probes(probes),
