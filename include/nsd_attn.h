@@ -159,7 +159,11 @@ int nsd_qk_norm_rope_store_strided(const void* q, int64_t q_row_stride, void* q_
  *     many pieces has a shorter longest piece;
  *   - one workgroup streams one piece; pieces are dealt longest first to
  *     the eight XCDs (workgroup i runs on XCD i % 8) with near-equal blocks
- *     and counts per XCD, each XCD's list longest first;
+ *     and counts per XCD, each XCD's list longest first, except that with
+ *     static_slots set, a list that puts two workgroups on some of the
+ *     XCD's C = static_slots / 16 CUs (positions j and j + C of the list
+ *     share a CU when the launch starts them together) pairs a long piece
+ *     with a short one on each such CU, so the CUs' totals are near-equal;
  *   - a segment cut into several pieces gets partials (normalised O in
  *     fp16, log2-sum-exp in fp32), merged in slot order by a second launch
  *     of the same call.

@@ -163,7 +163,8 @@ extern "C" int nsd_attn_plan_build_claimed(const int32_t* seq_ids, const int32_t
   //    segment, then piece order), each to the XCD with the fewest blocks
   //    among those holding fewer than ceil(pieces / 8), so the XCDs get
   //    near-equal work and list lengths that differ by at most one.  Each
-  //    XCD's list is then longest first, as the hardware dispatches it.
+  //    XCD's list is then longest first, as the hardware dispatches it, and
+  //    laid out per CU below.
   std::vector<std::pair<int64_t, int64_t>> all;  // (segment, piece index)
   all.reserve(n_pieces);
   for (int64_t s = 0; s < n_segs; ++s)
@@ -190,6 +191,29 @@ extern "C" int nsd_attn_plan_build_claimed(const int32_t* seq_ids, const int32_t
     const auto b = piece_blocks(pc.first, pc.second);
     load[x] += b.second - b.first;
     lists[x].push_back(pc);
+  }
+  //    The attention runs two workgroups per CU, and a launch whose static
+  //    workgroups all start at once puts positions j and j + C of an XCD's
+  //    list on one CU (C = the XCD's CUs, static_slots / 16): a CU streams
+  //    its two pieces at one combined rate, so it ends when their sum is
+  //    done.  Lists that need a second workgroup on some CUs are therefore
+  //    laid out so that every such CU runs a long piece first and a short
+  //    one beside it: the longest C pieces take the first positions, and the
+  //    CUs that also get one of the rest are those with the shortest first
+  //    pieces, the longest of them paired with the shortest of the rest.
+  if (static_slots >= 2 * kXcds) {
+    const size_t C = (size_t)(static_slots / kXcds / 2);
+    for (auto& lst : lists) {
+      if (lst.size() <= C || lst.size() > 2 * C) continue;
+      const size_t m = lst.size() - C;  // CUs that run two pieces
+      std::vector<std::pair<int64_t, int64_t>> o(lst.size());
+      for (size_t i = 0; i < C - m; ++i) o[m + i] = lst[i];
+      for (size_t i = 0; i < m; ++i) {
+        o[i] = lst[C - m + i];
+        o[C + i] = lst[lst.size() - 1 - i];
+      }
+      lst.swap(o);
+    }
   }
   const std::vector<std::pair<int64_t, int64_t>> claimed(all.begin() + n_static_pieces, all.end());
   const size_t longest = n_pieces > 0 ? cap : 0;

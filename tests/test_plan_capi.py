@@ -98,8 +98,13 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
     nblk = [(-(-(int(g[3]) + int(g[1])) // 16)) for g in groups for _ in range(hkv)]
     total = sum(nblk)
     # static records: one workgroup each, a multiple of the XCD count; each
-    # XCD's records (i, i + 8, ...) are its pieces longest first, empty ones
-    # last, and the XCDs' lists differ in length by at most one.  Claimed
+    # XCD's records (i, i + 8, ...) are its pieces, empty ones last, and the
+    # XCDs' lists differ in length by at most one.  A list is longest first,
+    # unless it puts a second workgroup on some of the XCD's C CUs (C =
+    # static slots / 16; positions j and j + C share a CU): then the CUs
+    # with one workgroup run the longest pieces, and each CU with two pairs
+    # one of the next-longest with one of the rest, longest with shortest
+    # (positions 0 .. m-1 longest first, C .. C+m-1 shortest first).  Claimed
     # records follow, longest first, none longer than a static one, with
     # half again as many workgroups (rounded up to 8) to claim them.
     n_static, n_claimed = p["static"], p["claimed"]
@@ -128,7 +133,15 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
         n_live_of.append(n_live)
         assert live[:n_live].all(), "empty records only at the end of an XCD list"
         sizes = (mine[:n_live, 2] - mine[:n_live, 1]).tolist()
-        assert sizes == sorted(sizes, reverse=True)
+        C = p["static_slots"] // (2 * XCDS)
+        if C and C < n_live <= 2 * C:
+            m = n_live - C
+            shared, lone, second = sizes[:m], sizes[m:C], sizes[C:]
+            assert lone == sorted(lone, reverse=True) and shared == sorted(shared, reverse=True)
+            assert second == sorted(second)
+            assert min(lone, default=max(shared)) >= max(shared) and min(shared) >= max(second)
+        else:
+            assert sizes == sorted(sizes, reverse=True)
         for rec in mine[:n_live]:
             h, bb, be, slot, row_start, q_len, sid, ctx, comb, cfirst, cslots, seg = (int(v) for v in rec)
             g = groups[seg // hkv]
@@ -341,6 +354,43 @@ def test_plan_xcd_lists_balance(lib):
     recs = p["records"]
     loads = [int((recs[x::8, 2] - recs[x::8, 1])[recs[x::8, 5] > 0].sum()) for x in range(8)]
     assert max(loads) - min(loads) <= max(-(-(int(c) + 5) // 16) for c in ctx)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_plan_pairs_pieces_per_cu(lib, seed):
+    """The verify shape on 512 slots (32 CUs per XCD, two workgroups each):
+    positions j and j + 32 of an XCD's list share a CU, and the largest CU
+    total is the smallest any pairing of that XCD's pieces allows (sorted
+    longest to shortest, the i-th longest paired with the i-th shortest
+    minimises the largest pair sum), below that of the plain longest-first
+    layout."""
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(256, 4097, 16)
+    sid = [i for i in range(16) for _ in range(5)]
+    sl = [int(c) + 1 + k for c in ctx for k in range(5)]
+    p, _ = _plan(sid, sl, workers=512, bt_rows=16, static_slots=512)
+    check_plan_invariants(p, sid, sl, 8, 4)
+    recs = p["records"]
+    for x in range(XCDS):
+        sz = (recs[x::XCDS, 2] - recs[x::XCDS, 1]).astype(int)
+        assert len(sz) == 64 and (sz > 0).all()
+        cu = sz[:32] + sz[32:]
+        srt = np.sort(sz)[::-1]
+        best = max(int(srt[i] + srt[63 - i]) for i in range(32))
+        plain = max(int(srt[i] + srt[32 + i]) for i in range(32))
+        assert int(cu.max()) == best <= plain
+        # brute force over every pairing on a small sample of the pieces
+        small = [int(v) for v in srt[::8]]  # 8 pieces, 105 pairings
+        def pairings(items):
+            if not items:
+                yield []
+                return
+            a = items[0]
+            for k in range(1, len(items)):
+                for rest in pairings(items[1:k] + items[k + 1:]):
+                    yield [(a, items[k])] + rest
+        opt = min(max(u + v for u, v in pr) for pr in pairings(small))
+        assert opt == max(small[i] + small[7 - i] for i in range(4))
 
 
 def _attention_with_plan(lib, words, hq=32, hkv=8, bt_rows=2, bt_stride=4096):
