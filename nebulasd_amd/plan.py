@@ -41,14 +41,17 @@ def num_workers(max_rows: int, device_index: int | None = None) -> int:
 
 
 # Pieces the planner cuts per workgroup slot.  One per slot binds every
-# piece to a workgroup and starts them all at once; more make the slots'
-# worth of longest pieces bound and the rest claimed at run time by the
-# workgroups that start as slots free up (a faster XCD takes more of them),
-# at the price of more pieces to start, merge and combine.  Measured
-# (graph-timed layer calls, one box, one run): verify 36.3 / 40.1 / 39.8 us
-# at 1 / 1.5 / 2 per slot, decode 63.2 / 64.0 / 62.8, ragged verify
-# (three 16-row tiles) 115.3 / 114.3 / 115.2.
-PIECES_PER_SLOT = {1: 2.0, 2: 1.0, 3: 1.5}
+# piece to a workgroup and starts them all at once, the planner pairing a
+# long piece with a short one on every CU; more make the slots' worth of
+# longest pieces bound and the rest claimed at run time by the workgroups
+# that start as slots free up (a faster XCD takes more of them), at the
+# price of more pieces to start, merge and combine.  Measured (graph-timed
+# layer calls, settings interleaved on one box): decode 54.3 / 57.5 us at
+# 1 / 2 per slot, ragged verify (three 16-row tiles) 104.4-109.4 /
+# 108.0-111.7 us at 1 / 1.5, verify 34.0 / 36.1 us at 1 / 1.25.  A batch
+# with more segments than slots still has its pieces beyond the slots
+# claimed (a segment is never shared by two pieces' worth of rows).
+PIECES_PER_SLOT = {1: 1.0, 2: 1.0, 3: 1.0}
 
 
 def pieces_for(slots: int, max_rows: int) -> int:

@@ -14,6 +14,7 @@ import torch
 import oracle
 from helpers import ATOL_LSE, ATOL_O, RTOL_O, assert_close, compact_cache
 from nebulasd_amd import _lib
+from nebulasd_amd import plan as planmod
 from nebulasd_amd.config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from nebulasd_amd.infer_state import build_infer_state, rope_cache
 from nebulasd_amd.kernels import paged_attention
@@ -199,13 +200,15 @@ def test_attention_no_rows(gpu):
 
 
 @pytest.mark.parametrize("q_len", [5, 1, 9], ids=["verify-bound", "decode-claimed", "q9-claimed"])
-def test_attention_graph_replay_bit_identical(gpu, q_len):
+def test_attention_graph_replay_bit_identical(gpu, q_len, monkeypatch):
     """A HIP graph of attention calls over every layer replays to the eager
     results bit for bit, replay after replay, with eager work in between.
-    Decode and 9-row groups cut more pieces than the device has workgroup
-    slots, so their later workgroups claim pieces from the workspace's
+    The decode and 9-row cases ask the planner for two pieces per workgroup
+    slot, so their later workgroups claim pieces from the workspace's
     counter, which every call (replayed or eager) must leave at zero."""
     print(f"graph replay, q_len {q_len}", flush=True)
+    if q_len != 5:
+        monkeypatch.setattr(planmod, "PIECES_PER_SLOT", 2.0)
     w = make_workload("target_verify", 9, device=gpu, pool_blocks=4096, num_layers=3,
                       ctxs=[3000, 40, 1500, 700, 9], q_len=q_len)
     mc = ModelConfig(w.spec.model)
