@@ -393,6 +393,31 @@ def test_plan_pairs_pieces_per_cu(lib, seed):
         assert opt == max(small[i] + small[7 - i] for i in range(4))
 
 
+@pytest.mark.parametrize("workers", [300, 400])
+def test_plan_pairs_with_single_piece_cus(lib, workers):
+    """Fewer pieces than slots: each XCD list of L pieces puts a second
+    workgroup on L - 32 of its 32 CUs; those CUs get the shortest first
+    pieces and each pairs its long piece with a short one, and the CUs with
+    one piece run the longest pieces."""
+    rng = np.random.default_rng(workers)
+    ctx = rng.integers(256, 4097, 16)
+    sid = [i for i in range(16) for _ in range(5)]
+    sl = [int(c) + 1 + k for c in ctx for k in range(5)]
+    p, _ = _plan(sid, sl, workers=workers, bt_rows=16, static_slots=512)
+    check_plan_invariants(p, sid, sl, 8, 4)
+    recs = p["records"]
+    for x in range(XCDS):
+        mine = recs[x::XCDS]
+        sz = (mine[:, 2] - mine[:, 1])[mine[:, 5] > 0].astype(int)
+        m = len(sz) - 32
+        assert 0 < m < 32
+        single, first, second = sz[m:32], sz[:m], sz[32:]
+        assert min(single) >= max(first) >= min(first) >= max(second)
+        # the doubled CUs' largest total is the least any pairing of those pieces allows
+        pool = np.sort(np.concatenate([first, second]))[::-1]
+        assert int((first + second).max()) == max(int(pool[i] + pool[2 * m - 1 - i]) for i in range(m))
+
+
 def _attention_with_plan(lib, words, hq=32, hkv=8, bt_rows=2, bt_stride=4096):
     """Call nsd_paged_attention with host buffers standing in for device ones.
 
