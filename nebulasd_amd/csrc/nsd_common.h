@@ -76,6 +76,7 @@ constexpr int kMaxGroupRows = 48;       // query rows of one segment: three 16-r
 constexpr int kMaxSlotsPerSegment = 128;
 constexpr int kMaxPieceBlocks = 256;    // blocks of one piece (four waves, one block id per lane)
 constexpr int kMinPieceBlocks = 4;
+constexpr int kWavesPerPiece = 4;       // waves of an attention workgroup (wave w: blocks w, w + 4, ...)
 constexpr int kXcds = 8;                // workgroup i of a launch runs on XCD i % 8
 
 // Attention workspace: the claim counter of plans with claimed records

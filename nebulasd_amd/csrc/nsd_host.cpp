@@ -154,9 +154,19 @@ extern "C" int nsd_attn_plan_build_claimed(const int32_t* seq_ids, const int32_t
       std::push_heap(heap.begin(), heap.end(), shorter);
     }
   }
+  //    Piece k of a segment of nb blocks cut into n starts at k * nb / n
+  //    rounded to a multiple of the workgroup's four waves (wave w streams
+  //    blocks w, w + 4, ...), so that every piece but the segment's last
+  //    gives its waves equal block counts and none waits for another at the
+  //    merge; the pieces stay within three blocks of nb / n (ceil(nb / n)
+  //    + 3 <= 256 is required, else the cut is the plain one).
   auto piece_blocks = [&](int64_t s, int64_t k) {
     const int64_t nb = seg_start[s + 1] - seg_start[s], n = seg_pieces[s];
-    return std::make_pair(k * nb / n, (k + 1) * nb / n);
+    if (nb > (kMaxPieceBlocks - kWavesPerPiece) * n) return std::make_pair(k * nb / n, (k + 1) * nb / n);
+    auto start = [&](int64_t j) {
+      return j >= n ? nb : (j * nb / n + kWavesPerPiece / 2) / kWavesPerPiece * kWavesPerPiece;
+    };
+    return std::make_pair(start(k), start(k + 1));
   };
 
   // 4. pieces to XCDs (workgroup i runs on XCD i % 8): longest first (ties:

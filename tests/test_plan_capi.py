@@ -174,8 +174,12 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
             for t, (m, nt) in enumerate(zip(n_of, nblk)):
                 if m < hi[t]:
                     assert nt * (n - 1) <= nb * m, (s, t)
-    # near-equal pieces per segment; partial slots in segment order exactly
-    # for segments cut into several pieces
+    # pieces per segment near nb / k, every piece start on a multiple of the
+    # workgroup's four waves and within two blocks of j * nb / k (so only the
+    # segment's last piece leaves its waves unequal block counts), unless the
+    # pieces are too long for that (then within one block of each other);
+    # partial slots in segment order exactly for segments cut into several
+    # pieces
     combined = {(int(c[3]), int(c[0])): (int(c[1]), int(c[2])) for c in p["combines"]}
     next_slot = 0
     for seg in sorted(pieces_of):
@@ -183,7 +187,14 @@ def check_plan_invariants(p, seq_ids, seq_lens, hkv, gqa):
         k = len(ps)
         assert k <= MAX_SLOTS
         sizes = [be - bb for bb, be, *_ in ps]
-        assert max(sizes) - min(sizes) <= 1
+        nb = nblk[seg]
+        if nb <= (MAX_PIECE_BLOCKS - 4) * k:
+            starts = [bb for bb, *_ in ps]
+            assert all(s0 % 4 == 0 for s0 in starts)
+            assert all(abs(s0 - j * nb / k) <= 2 for j, s0 in enumerate(starts))
+            assert min(sizes) >= 1 and max(sizes) <= MAX_PIECE_BLOCKS
+        else:
+            assert max(sizes) - min(sizes) <= 1
         key = (int(groups[seg // hkv][0]), seg % hkv)
         if k == 1:
             assert ps[0][2:] == (-1, -1, 0, 0) and key not in combined
@@ -320,7 +331,7 @@ def test_plan_respects_kernel_limits(lib):
     # waves, one block id per lane), so 4000 blocks take 16 pieces per kv head
     p, _ = _plan([0], [16 * 4000], workers=1, stride=4096)
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
-    assert p["piece_blocks"] == 250 and p["max_blocks"] == 250
+    assert p["piece_blocks"] == 250 and 250 <= p["max_blocks"] <= MAX_PIECE_BLOCKS
     assert len(p["pieces"]) == 8 * 16
 
 
