@@ -16,12 +16,13 @@
 // product, and a row's online-softmax state lives in one lane column.
 //
 // Work split.  The host planner cuts every segment into near-equal pieces
-// of 16-token blocks; one workgroup of four waves streams one piece.  The
-// pieces that fit the device's workgroup slots are bound to workgroups
-// ahead of the launch (workgroup i runs on XCD i % 8; the two pieces that
-// share a CU pair a long one with a short one); any more are claimed at run
-// time, one device-scope add
-// per later workgroup, so an XCD whose slots free up early takes more.
+// of 16-token blocks (starting on multiples of four blocks, so the waves get
+// equal counts); one workgroup of four waves streams one piece.  The pieces
+// that fit the device's workgroup slots are bound to workgroups ahead of
+// the launch (workgroup i runs on XCD i % 8; the two pieces that share a CU
+// pair a long one with a short one); any more (more segments than slots)
+// are claimed at run time, one device-scope add per later workgroup, so an
+// XCD whose slots free up early takes more.
 // Wave w streams blocks w, w + 4, ... of the piece: it brings each block's
 // K tile and V tile (4 KB each) straight from HBM into its own LDS double
 // buffer with global_load_lds_dwordx4 and computes the previous block while
