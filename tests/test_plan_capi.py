@@ -333,6 +333,12 @@ def test_plan_respects_kernel_limits(lib):
     check_plan_invariants(p, [0], [16 * 4000], 8, 4)
     assert p["piece_blocks"] == 250 and 250 <= p["max_blocks"] <= MAX_PIECE_BLOCKS
     assert len(p["pieces"]) == 8 * 16
+    # 255 blocks per piece: starts rounded to multiples of four could make a
+    # piece longer than 256, so the cut stays the plain near-equal one
+    p, _ = _plan([0], [16 * 4080], workers=1, stride=4096)
+    check_plan_invariants(p, [0], [16 * 4080], 8, 4)
+    sizes = sorted({int(r[2] - r[1]) for r in p["pieces"]})
+    assert sizes == [255] and len(p["pieces"]) == 8 * 16
 
 
 @pytest.mark.parametrize("slots", [64, 100, 512])
