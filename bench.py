@@ -10,7 +10,8 @@ the stream the kernels run on: ``value`` is µs per layer call (all timed
 calls), ``ms_per_step`` ms per pass, and the per-pass median / p10 / p90 are
 reported beside it, with a same-layer "hot" figure (every call on layer 0,
 whose blocks stay cached) as a diagnostic.  The fused prologue (QK-RMSNorm +
-RoPE + KV store) is timed alone and together with the attention.
+RoPE + KV store) is timed alone, followed by the attention (two launches per
+layer), and inside the attention's own launch (one launch per layer).
 
 Beside the headline: Draft decode (Qwen3-0.6B shape, B=64), ragged
 long-context verify (q_len=9, contexts log-U[1024, 32768]) and the small
@@ -110,16 +111,17 @@ def _spread(per_replay, calls_per_replay: int) -> dict:
 def measure(name: str, seed: int, steps: int, warmup: int):
     """Time `steps` passes over the layers for workload `name`; returns (result dict, workload).
 
-    Three graphs of one pass over all layers are timed: the attention alone
-    (the headline), the fused prologue alone, and prologue + attention as a
-    layer runs them.  The prologue works on copies of q and fresh k/v rows,
-    so the attention inputs of the first graph are never modified.
+    Four graphs of one pass over all layers are timed: the attention alone
+    (the headline), the fused prologue alone, prologue then attention (two
+    launches per layer), and both in the attention's launch
+    (paged_attention_fused).  The prologue works on copies of q and fresh
+    k/v rows, so the attention inputs of the first graph are never modified.
     """
     import torch
 
     from nebulasd_amd.config import EngineConfig, ModelConfig
     from nebulasd_amd.infer_state import build_infer_state, rope_cache
-    from nebulasd_amd.kernels import paged_attention, qk_norm_rope_store
+    from nebulasd_amd.kernels import paged_attention, paged_attention_fused, qk_norm_rope_store
     from nebulasd_amd.workload import make_workload
 
     dev = torch.device("cuda:0")
@@ -153,6 +155,11 @@ def measure(name: str, seed: int, steps: int, warmup: int):
                                st, layer, cos, sin)
             paged_attention(qp, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, o)
 
+    def fused_pass():
+        for layer in range(L):
+            paged_attention_fused(w.q, kn, vn, w.k_cache, w.v_cache, w.block_table, qw, kw, mc, ec, st, layer,
+                                  cos, sin, o)
+
     def hot_pass():
         for _ in range(L):
             paged_attention(w.q, w.k_cache, w.v_cache, w.block_table, mc, ec, st, 0, o)
@@ -165,6 +172,7 @@ def measure(name: str, seed: int, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     us_pro, per_pro = _time_graph(prologue_pass, stream, reps, wreps)
     us_layer, per_layer = _time_graph(layer_pass, stream, reps, wreps)
+    us_fused, per_fused = _time_graph(fused_pass, stream, reps, wreps)
     # Diagnostic only: every call reads layer 0, whose blocks then stay in
     # the 256 MB Infinity Cache between calls.
     us_hot, _ = _time_graph(hot_pass, stream, reps, wreps)
@@ -195,6 +203,8 @@ def measure(name: str, seed: int, steps: int, warmup: int):
         "prologue_gbps": w.prologue_bytes() / (us_pro / L * 1e-6) / 1e9,
         "prologue_plus_attention_us": us_layer / L,
         "prologue_plus_attention_us_spread": _spread(per_layer, L),
+        "fused_layer_us": us_fused / L,
+        "fused_layer_us_spread": _spread(per_fused, L),
     }
     return res, w
 
@@ -1379,7 +1389,8 @@ LINE_MAX_BYTES = 7500
 LEG_KEYS = ("us_per_layer_call", "hbm_gbps", "hbm_frac", "frac_of_gather_floor", "frac_of_same_mechanism_floor",
             "tflops", "mfma_frac",
             "us_per_write", "reference_us_per_write", "us_per_layer", "floor_us_at_copy_rate",
-            "reference_sdpa_loop_us", "us_per_call", "reference_us_per_call", "us_per_call_graph")
+            "reference_sdpa_loop_us", "us_per_call", "reference_us_per_call", "us_per_call_graph",
+            "prologue_plus_attention_us", "fused_layer_us")
 # Second-level dicts of a leg whose scalar figures are kept as well.
 LEG_SUBKEYS = ("kv_gather_floor", "native_decoder_stack", "throughput", "draft", "target", "D2H", "H2D")
 
@@ -1395,6 +1406,12 @@ def _compact_cpu(c):
     if not isinstance(c, dict):
         return None
     return {k: _sig(c[k]) for k in ("value", "unit", "cores", "kind") if k in c}
+
+
+def _layer_note(r: dict) -> str:
+    """Prologue + attention per layer: two launches, and one fused launch."""
+    return (f"; with the prologue {r['prologue_plus_attention_us']:.2f} us (two launches), "
+            f"{r['fused_layer_us']:.2f} us (one fused launch)")
 
 
 def _scalars(d: dict, keys) -> dict:
@@ -1504,7 +1521,7 @@ def main():
         with_gather_floor(res, w, args.steps, args.warmup)
     print(f"# {args.workload}: {res['us_per_layer_call']:.2f} us/layer-call, "
           f"{res['hbm_gbps']:.0f} GB/s" + (f" (K/V gather floor {res['kv_gather_floor']['us_per_layer_call']:.2f} us)"
-                                          if args.probes else ""), file=sys.stderr, flush=True)
+                                          if args.probes else "") + _layer_note(res), file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_baseline_seconds > 0:
         cpu = cpu_baseline(w, args.cpu_baseline_seconds)
@@ -1519,7 +1536,7 @@ def main():
         if args.probes:
             with_gather_floor(r2, w2, args.steps, args.warmup)
         print(f"# {name}: {r2['us_per_layer_call']:.2f} us/layer-call, "
-              f"{r2['hbm_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+              f"{r2['hbm_gbps']:.0f} GB/s" + _layer_note(r2), file=sys.stderr, flush=True)
         if args.cpu_baseline_seconds > 0:
             r2["cpu_baseline"] = cpu_baseline(w2, args.other_cpu_seconds)
         secondary[name] = r2

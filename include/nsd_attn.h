@@ -234,6 +234,37 @@ int nsd_paged_attention(const void* q, void* o, float* lse, const void* k_cache,
                         int32_t* status, void* stream);
 
 /*
+ * nsd_paged_attention_fused: the layer's prologue and its attention in one
+ * launch.  Replaces the sequence nsd_qk_norm_rope_store (transformer_layer.py
+ * :114-145: QK-RMSNorm, RoPE at position seq_len - 1, K/V into the cache
+ * slot) then nsd_paged_attention, with identical results: o, lse and the
+ * cache rows written are bit for bit those of the two calls (q itself is
+ * not written back).  The rows' q, k and v are either fp16 rows (q, k, v
+ * with row strides in elements; each 16-byte aligned, each stride a
+ * multiple of 8) or, when partials != NULL, the fused q/k/v projection's
+ * fp32 split partials [splits][rows][(Hq + 2 Hkv) * 128] (nsd_linear_partials), summed
+ * in split order and rounded to fp16 first.  q_norm_w / k_norm_w: [128]
+ * fp16 (both or neither), cos/sin: [n_positions, 64] fp16, all 16-byte
+ * aligned.  The rows are the plan's (the plan carries each group's sequence
+ * and positions).  Each workgroup builds its query rows itself, and the
+ * workgroup that streams a cache block holding a new row writes that row
+ * before it loads the block.  So the plan must keep every sequence's rows
+ * in one verify group: a plan that splits a sequence over several groups
+ * returns NSD_ERR_UNSUPPORTED (run the two calls instead), and positions
+ * past the RoPE tables return NSD_ERR_INVALID, before any launch.  The
+ * other arguments, the workspace and the status word are nsd_paged_attention's.
+ */
+int nsd_paged_attention_fused(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+                              const void* v, int64_t v_row_stride, const float* partials, int splits,
+                              const void* q_norm_w, const void* k_norm_w, float eps,
+                              const void* cos_cache, const void* sin_cache, int64_t n_positions, void* o,
+                              float* lse, void* k_cache, void* v_cache, int64_t num_blocks, int num_layers,
+                              int layer, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                              const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
+                              const int32_t* plan_host, const int32_t* plan_dev, void* workspace,
+                              int64_t workspace_bytes, float softmax_scale, int32_t* status, void* stream);
+
+/*
  * nsd_paged_attention_noalloc: nsd_paged_attention without a workspace
  * argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It

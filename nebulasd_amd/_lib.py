@@ -67,6 +67,12 @@ SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
                 c_int, c_int, c_int, c_void_p, c_int64, c_int64, _I32P, c_void_p, c_void_p,
                 c_int64, c_float, c_void_p, c_void_p]),
+    "nsd_paged_attention_fused": (
+        c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int,
+                c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_int,
+                c_void_p, c_int64, c_int64, _I32P, c_void_p, c_void_p, c_int64, c_float,
+                c_void_p, c_void_p]),
     "nsd_paged_attention_noalloc": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int,
                 c_int, c_int, c_int, c_void_p, c_int64, c_int64, _I32P, c_void_p, c_float,

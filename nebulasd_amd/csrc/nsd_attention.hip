@@ -49,7 +49,9 @@
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB
 //   contiguous at ((blk*L + layer)*Hkv + head)*16*128 (:49-50, :70-71).
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "nsd_device.h"
 
@@ -253,9 +255,34 @@ struct PieceTable {
   uint32_t e[kPieceTableMax];
 };
 
-template <int NT>
+// The fused prologue (nsd_paged_attention_fused): the rows' q, k and v as
+// the q/k/v projection left them, either fp16 rows (row strides in
+// elements) or that projection's fp32 split partials [splits][rows][(Hq +
+// 2 Hkv) * D] summed in split order and rounded to fp16 (the GEMM output
+// rounding); the QK-norm weights (or null), the RoPE tables and the caches
+// the new K/V rows are written to.
+struct FusedArgs {
+  const f16* q;
+  const f16* k;
+  const f16* v;
+  int64_t q_rs, k_rs, v_rs;
+  const float* part;
+  int64_t part_rs, split_stride;
+  int splits;
+  const f16* qn;
+  const f16* kn;
+  float eps;
+  const f16* cos_c;
+  const f16* sin_c;
+  f16* kc;
+  f16* vc;
+};
+struct NoFused {};
+
+template <int NT, class Extra = NoFused>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void paged_attn_kernel(AttnArgs a, PieceTable pt) {
+void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
+  constexpr bool FUSED = std::is_same_v<Extra, FusedArgs>;
   extern __shared__ __align__(16) char smem_raw[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -350,20 +377,183 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt) {
   // landed (the builtin also tells the compiler its own loads are done, so
   // it inserts no wait for them inside the loop, which would drain the
   // buffer loads too: vmcnt retires in order).
+  //
+  // Fused prologue.  Rows are computed in the layout of the score MFMA's B
+  // operand: lane (lg, lr) holds dims 32kk + 8lg .. +7 of its row (kk < 4),
+  // so dims d and d + 64 (a RoPE pair) sit in one lane.  The prologue sums
+  // x_d^2 + x_{d+64}^2 over a butterfly of lanes d ^ 32, ^ 16, ^ 8, ^ 4, ^ 2,
+  // ^ 1; here that is the same tree: in the lane over kk, across lanes l ^ 32
+  // and l ^ 16 (the lg bits), then in the lane over j.  Every value is then
+  // the prologue's, bit for bit.
+  //
+  // New K/V rows: token i of the group sits at position ctx + i of its
+  // sequence, in block (ctx + i) / 16.  The wave that streams such a block
+  // writes the block's new rows (lane row lr: token own_lo + lr) and has
+  // those stores done before it issues the block's DMA: before its first two
+  // blocks' loads when the block is one of those, else under the start's
+  // wait.  The tokens span at most four consecutive blocks, so a wave owns
+  // at most one of them.
+  int own_jj = -1, own_lo = 0, own_hi = 0;
+  if constexpr (FUSED) {
+    const int b_first = ctx / BS, b_last = (ctx + q_len - 1) / BS;
+    for (int b = b_first; b <= b_last; ++b) {
+      const int rel = b - blk0;
+      if (rel >= 0 && rel < nb && (rel & (kWaves - 1)) == wave) {
+        own_jj = rel / kWaves;
+        own_lo = b * BS - ctx > 0 ? b * BS - ctx : 0;
+        own_hi = (b + 1) * BS - ctx < q_len ? (b + 1) * BS - ctx : q_len;
+      }
+    }
+  }
+  // a bad block is flagged above and gets no stores
+  const bool own = FUSED && own_jj >= 0 && !((bad_mask >> own_jj) & 1);
+  // One row of head hd (Hq q heads, then Hkv k, then Hkv v) of the q/k/v
+  // projection's fp16 output, in the row layout.
+  auto load_row = [&](int64_t r, int hd, f16x8 (&h)[4]) __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+      if (fx.part == nullptr) {
+        const f16* src = hd < a.hq ? fx.q + r * fx.q_rs + (int64_t)hd * D
+                         : hd < a.hq + a.hkv ? fx.k + r * fx.k_rs + (int64_t)(hd - a.hq) * D
+                                             : fx.v + r * fx.v_rs + (int64_t)(hd - a.hq - a.hkv) * D;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) h[kk] = *reinterpret_cast<const f16x8*>(src + 32 * kk + 8 * lg);
+      } else {
+        const float* prow = fx.part + r * fx.part_rs + (int64_t)hd * D;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          f32x4 s0 = *reinterpret_cast<const f32x4*>(prow + 32 * kk + 8 * lg);
+          f32x4 s1 = *reinterpret_cast<const f32x4*>(prow + 32 * kk + 8 * lg + 4);
+          for (int s2 = 1; s2 < fx.splits; ++s2) {
+            s0 += *reinterpret_cast<const f32x4*>(prow + s2 * fx.split_stride + 32 * kk + 8 * lg);
+            s1 += *reinterpret_cast<const f32x4*>(prow + s2 * fx.split_stride + 32 * kk + 8 * lg + 4);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            h[kk][j] = f16_of(s0[j]);
+            h[kk][j + 4] = f16_of(s1[j]);
+          }
+        }
+      }
+    }
+  };
+  // the norm weights of a row (any readable row when there is no norm)
+  auto load_w = [&](const f16* w, f16x8 (&w8)[4]) __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+      const f16* src = w != nullptr ? w : fx.cos_c;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) w8[kk] = *reinterpret_cast<const f16x8*>(src + 32 * kk + 8 * lg);
+    }
+  };
+  // the RoPE angles of position pos: cos dims 0..63 in cs[0..1], sin in cs[2..3]
+  auto load_cs = [&](int64_t pos, f16x8 (&cs)[4]) __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        cs[kk] = *reinterpret_cast<const f16x8*>(fx.cos_c + pos * (D / 2) + 32 * kk + 8 * lg);
+        cs[kk + 2] = *reinterpret_cast<const f16x8*>(fx.sin_c + pos * (D / 2) + 32 * kk + 8 * lg);
+      }
+    }
+  };
+  // h RMS-normalised with weights w8 when `norm`, then rotated by cs
+  auto norm_rope = [&](const f16x8 (&h)[4], bool norm, const f16x8 (&w8)[4], const f16x8 (&cs)[4],
+                       f16x8 (&out)[4]) __attribute__((always_inline)) {
+    if constexpr (!FUSED) return;
+    float x[4][8];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[kk][j] = (float)h[kk][j];
+    if (norm) {
+      float u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] = sq_pair(x[0][j], x[2][j]) + sq_pair(x[1][j], x[3][j]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] += __shfl_xor(u[j], 32, kWave);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] += __shfl_xor(u[j], 16, kWave);
+      const float ss = ((u[0] + u[4]) + (u[2] + u[6])) + ((u[1] + u[5]) + (u[3] + u[7]));
+      float eps = 0.f;
+      if constexpr (FUSED) eps = fx.eps;
+      const float rstd = 1.f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[kk][j] = (float)f16_of(x[kk][j] * rstd * (float)w8[kk][j]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float c = (float)cs[kk][j], sn = (float)cs[kk + 2][j];
+        out[kk][j] = f16_of(rope_lo(x[kk][j], x[kk + 2][j], c, sn));
+        out[kk + 2][j] = f16_of(rope_hi(x[kk][j], x[kk + 2][j], c, sn));
+      }
+  };
+  f16x8 nk[4], nv[4], nkw[4], ncs[4];  // the new rows' k, v, k-norm weights, angles
+  auto load_new = [&]() __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+      const int i = own_lo + lr < own_hi ? own_lo + lr : own_lo;
+      load_row(row_start + i, a.hq + head, nk);
+      load_row(row_start + i, a.hq + a.hkv + head, nv);
+      load_w(fx.kn, nkw);
+      load_cs(ctx + i, ncs);
+    }
+  };
+  auto store_new = [&]() __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+      f16x8 ko[4];
+      norm_rope(nk, fx.kn != nullptr, nkw, ncs, ko);
+      if (own_lo + lr < own_hi) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)boff, own_jj);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)boff >> 32), own_jj);
+        const int64_t at = (int64_t)(((uint64_t)hi << 32) | lo) + (int64_t)((ctx + own_lo + lr) % BS) * D;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          *reinterpret_cast<f16x8*>(fx.kc + at + 32 * kk + 8 * lg) = ko[kk];
+          *reinterpret_cast<f16x8*>(fx.vc + at + 32 * kk + 8 * lg) = nv[kk];
+        }
+      }
+    }
+  };
+  const bool own_early = own && own_jj <= 1;
+  if (own_early) {
+    load_new();
+    store_new();
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the new rows are in the cache before their block's DMA
+  }
   if (my_n > 0) issue(0);
   if (my_n > 1) issue(1);
   // Query rows of each row tile as the B operand of the score MFMA (lane
   // (lg, lr): dims 32kk + 8lg .. +7 of row lr); rows past the group read its
   // row 0 and are never stored.
   f16x8 qf[NT][4];
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int n = 16 * t + lr;
-    const int nr = n < n_rows ? n : 0;
-    const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
-    const f16* qrow = a.q + ((int64_t)(row_start + qi) * a.hq + head * a.gqa + gh) * D;
+    for (int t = 0; t < NT; ++t) {
+      const int n = 16 * t + lr;
+      const int nr = n < n_rows ? n : 0;
+      const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
+      const f16* qrow = a.q + ((int64_t)(row_start + qi) * a.hq + head * a.gqa + gh) * D;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *reinterpret_cast<const f16x8*>(qrow + 32 * kk + 8 * lg);
+      for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *reinterpret_cast<const f16x8*>(qrow + 32 * kk + 8 * lg);
+    }
+  } else {
+    // every load first (the new rows', the query rows'), then the arithmetic
+    const bool own_late = own && !own_early;
+    if (own_late) load_new();
+    f16x8 qh[NT][4], qcs[NT][4], qw[4];
+    load_w(fx.qn, qw);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int n = 16 * t + lr;
+      const int nr = n < n_rows ? n : 0;
+      const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
+      load_row(row_start + qi, head * a.gqa + gh, qh[t]);
+      load_cs(ctx + qi, qcs[t]);
+    }
+    if (own_late) store_new();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) norm_rope(qh[t], fx.qn != nullptr, qw, qcs[t], qf[t]);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
@@ -511,14 +701,22 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt) {
 
 template <int NT>
 int launch_nt(const AttnArgs& args, const PieceTable& pt, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(paged_attn_kernel<NT>, dim3(grid), dim3(kThreads), kLdsBytes, stream, args, pt);
+  hipLaunchKernelGGL((paged_attn_kernel<NT, NoFused>), dim3(grid), dim3(kThreads), kLdsBytes, stream, args, pt,
+                     NoFused{});
   return launch_status("paged_attention");
+}
+
+template <int NT>
+int launch_nt_fused(const AttnArgs& args, const PieceTable& pt, const FusedArgs& f, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_attn_kernel<NT, FusedArgs>), dim3(grid), dim3(kThreads), kLdsBytes, stream, args, pt,
+                     f);
+  return launch_status("paged_attention_fused");
 }
 
 template <int NT>
 int occupancy_nt(int* blocks) {
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-             blocks, reinterpret_cast<const void*>(&paged_attn_kernel<NT>), kThreads, kLdsBytes) == hipSuccess
+             blocks, reinterpret_cast<const void*>(&paged_attn_kernel<NT, NoFused>), kThreads, kLdsBytes) == hipSuccess
              ? NSD_OK
              : NSD_ERR_HIP;
 }
@@ -563,7 +761,7 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
                          const int32_t* block_table, int64_t bt_rows, int64_t bt_stride,
                          const int32_t* plan_host, const int32_t* plan_dev, void* part,
                          int64_t part_capacity, float softmax_scale, int32_t* status,
-                         void* stream) {
+                         void* stream, const FusedArgs* fused = nullptr) {
   if (head_dim != D) return fail(NSD_ERR_UNSUPPORTED, "paged_attention: head_dim=%d (only 128)", head_dim);
   if (block_size != BS)
     return fail(NSD_ERR_UNSUPPORTED, "paged_attention: block_size=%d (only 16)", block_size);
@@ -583,9 +781,9 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
   const int rows_max = plan_host[kPlanRowsMax];
   const int n_rows_plan = plan_host[kPlanRows];
   if (n_rows_plan == 0 || grid == 0) return NSD_OK;
-  if (!q || !o || !k_cache || !v_cache || !block_table)
+  if ((!q && !fused) || !o || !k_cache || !v_cache || !block_table)
     return fail(NSD_ERR_INVALID, "paged_attention: null pointer");
-  if (!aligned16(q) || !aligned16(o) || !aligned16(k_cache) || !aligned16(v_cache))
+  if ((!fused && !aligned16(q)) || !aligned16(o) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(NSD_ERR_INVALID, "paged_attention: q/o/caches must be 16-byte aligned");
   const int nt = (rows_max + 15) / 16;
   const int64_t n_slots = plan_host[kPlanSlots];
@@ -680,7 +878,11 @@ int paged_attention_impl(const void* q, void* o, float* lse, const void* k_cache
     }
     pt.e[i] = (uint32_t)sid | (uint32_t)b0 << 16;
   }
-  const int rc = nt == 1 ? launch_nt<1>(args, pt, grid, st)
+  const int rc = fused != nullptr
+                     ? (nt == 1   ? launch_nt_fused<1>(args, pt, *fused, grid, st)
+                        : nt == 2 ? launch_nt_fused<2>(args, pt, *fused, grid, st)
+                                  : launch_nt_fused<3>(args, pt, *fused, grid, st))
+                 : nt == 1 ? launch_nt<1>(args, pt, grid, st)
                  : nt == 2 ? launch_nt<2>(args, pt, grid, st)
                            : launch_nt<3>(args, pt, grid, st);
   if (rc != NSD_OK || n_combine == 0) return rc;
@@ -746,6 +948,80 @@ extern "C" int nsd_paged_attention(const void* q, void* o, float* lse, const voi
                               num_q_heads, num_kv_heads, head_dim, block_size, block_table,
                               bt_rows, bt_stride, plan_host, plan_dev, workspace, workspace_bytes,
                               softmax_scale, status, stream);
+}
+
+extern "C" int nsd_paged_attention_fused(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+                                         const void* v, int64_t v_row_stride, const float* partials, int splits,
+                                         const void* q_norm_w, const void* k_norm_w, float eps,
+                                         const void* cos_cache, const void* sin_cache, int64_t n_positions, void* o,
+                                         float* lse, void* k_cache, void* v_cache, int64_t num_blocks,
+                                         int num_layers, int layer, int num_q_heads, int num_kv_heads, int head_dim,
+                                         int block_size, const int32_t* block_table, int64_t bt_rows,
+                                         int64_t bt_stride, const int32_t* plan_host, const int32_t* plan_dev,
+                                         void* workspace, int64_t workspace_bytes, float softmax_scale,
+                                         int32_t* status, void* stream) {
+  if (!plan_host) return fail(NSD_ERR_INVALID, "paged_attention_fused: null plan");
+  if (plan_host[kPlanMagic] != kPlanMagicValue || plan_host[kPlanVersion] != kPlanVersionValue)
+    return fail(NSD_ERR_INVALID, "paged_attention_fused: not a plan (bad magic/version)");
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(NSD_ERR_INVALID, "paged_attention_fused: num_q_heads=%d, num_kv_heads=%d", num_q_heads,
+                num_kv_heads);
+  const int64_t rows = plan_host[kPlanRows];
+  const int64_t heads = (int64_t)num_q_heads + 2 * num_kv_heads;
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(NSD_ERR_INVALID, "paged_attention_fused: pass both norm weights or neither");
+  if (!cos_cache || !sin_cache || n_positions <= 0 || !aligned16(cos_cache) || !aligned16(sin_cache) ||
+      (q_norm_w && (!aligned16(q_norm_w) || !aligned16(k_norm_w))))
+    return fail(NSD_ERR_INVALID, "paged_attention_fused: RoPE tables and norm weights must be 16-byte aligned");
+  if (partials != nullptr) {
+    if (splits < 1 || splits > 16 || !aligned16(partials))
+      return fail(NSD_ERR_INVALID, "paged_attention_fused: splits=%d (1..16), partials 16-byte aligned", splits);
+  } else if (!q || !k || !v || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+             q_row_stride < (int64_t)num_q_heads * D || k_row_stride < (int64_t)num_kv_heads * D ||
+             v_row_stride < (int64_t)num_kv_heads * D || q_row_stride % 8 != 0 || k_row_stride % 8 != 0 ||
+             v_row_stride % 8 != 0) {
+    return fail(NSD_ERR_INVALID,
+                "paged_attention_fused: q/k/v rows (16-byte aligned, strides multiples of 8 covering the heads)");
+  }
+  // every sequence's new rows in one group, so that no workgroup reads a new
+  // row another one writes in the same launch; every position in the tables
+  const int n_groups = plan_host[kPlanGroups];
+  const int32_t* grp = plan_host + plan_host[kPlanOffGroups];
+  std::vector<int32_t> sids;
+  sids.reserve(n_groups);
+  for (int g = 0; g < n_groups; ++g) {
+    const int32_t* gr = grp + 4 * g;
+    if ((int64_t)gr[3] + gr[1] > n_positions)
+      return fail(NSD_ERR_INVALID, "paged_attention_fused: position %lld outside the %lld-row RoPE tables",
+                  (long long)gr[3] + gr[1] - 1, (long long)n_positions);
+    sids.push_back(gr[2]);
+  }
+  std::sort(sids.begin(), sids.end());
+  if (std::adjacent_find(sids.begin(), sids.end()) != sids.end())
+    return fail(NSD_ERR_UNSUPPORTED,
+                "paged_attention_fused: a sequence's rows span several verify groups (run the prologue, then "
+                "paged_attention)");
+  FusedArgs f;
+  f.q = static_cast<const f16*>(q);
+  f.k = static_cast<const f16*>(k);
+  f.v = static_cast<const f16*>(v);
+  f.q_rs = q_row_stride;
+  f.k_rs = k_row_stride;
+  f.v_rs = v_row_stride;
+  f.part = partials;
+  f.part_rs = heads * D;
+  f.split_stride = rows * heads * D;
+  f.splits = splits;
+  f.qn = static_cast<const f16*>(q_norm_w);
+  f.kn = static_cast<const f16*>(k_norm_w);
+  f.eps = eps;
+  f.cos_c = static_cast<const f16*>(cos_cache);
+  f.sin_c = static_cast<const f16*>(sin_cache);
+  f.kc = static_cast<f16*>(k_cache);
+  f.vc = static_cast<f16*>(v_cache);
+  return paged_attention_impl(nullptr, o, lse, k_cache, v_cache, num_blocks, num_layers, layer, num_q_heads,
+                              num_kv_heads, head_dim, block_size, block_table, bt_rows, bt_stride, plan_host,
+                              plan_dev, workspace, workspace_bytes, softmax_scale, status, stream, &f);
 }
 
 extern "C" int nsd_paged_attention_noalloc(const void* q, void* o, float* lse,

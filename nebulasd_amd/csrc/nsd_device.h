@@ -20,6 +20,23 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// The QK-norm's x_d^2 + x_{d+64}^2 and the rotate-half RoPE pair with the
+// fused multiply-adds spelled out, so that every kernel computing them (the
+// prologue, the attention that runs it fused) rounds identically, whatever
+// the compiler would contract on its own.
+__device__ inline float sq_pair(float a, float b) { return __builtin_fmaf(a, a, b * b); }
+__device__ inline float rope_lo(float x0, float x1, float c, float s) { return __builtin_fmaf(x0, c, -(x1 * s)); }
+__device__ inline float rope_hi(float x0, float x1, float c, float s) { return __builtin_fmaf(x0, s, x1 * c); }
+// fp32 value x rounded to fp16.  The empty asm pins x as an fp32 register, so
+// the conversion stays a separate step: left alone, the compiler folds it into
+// a mixed-precision FMA (v_fma_mixlo_f16 / v_fma_mixhi_f16) in some kernels
+// and not in others, and the two can differ in the last place.  (Not
+// volatile: a volatile asm would also order the memory operations around it.)
+__device__ inline f16 f16_of(float x) {
+  asm("" : "+v"(x));
+  return (f16)x;
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);

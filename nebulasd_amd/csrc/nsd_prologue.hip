@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
     const float* p = part + r * q_stride + (int64_t)hd * D + c;
     float acc = p[0];
     for (int q2 = 1; q2 < splits; ++q2) acc += p[q2 * split_stride];
-    return (f16)acc;
+    return f16_of(acc);
   };
 
   int64_t slot = -1;  // element offset of (block, layer, head 0, pos % BS, 0)
@@ -207,14 +207,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
     x1 = (float)xin[lane + 64];
   }
   if (w != nullptr) {
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float ss = wave_sum(sq_pair(x0, x1));
     const float rstd = 1.f / sqrtf(ss / (float)D + eps);
-    x0 = (float)(f16)(x0 * rstd * (float)w[lane]);
-    x1 = (float)(f16)(x1 * rstd * (float)w[lane + 64]);
+    x0 = (float)f16_of(x0 * rstd * (float)w[lane]);
+    x1 = (float)f16_of(x1 * rstd * (float)w[lane + 64]);
   }
   const float c = (float)cos_c[pos * (D / 2) + lane], s = (float)sin_c[pos * (D / 2) + lane];
-  const f16 y0 = (f16)(x0 * c - x1 * s);
-  const f16 y1 = (f16)(x0 * s + x1 * c);
+  const f16 y0 = f16_of(rope_lo(x0, x1, c, s));
+  const f16 y1 = f16_of(rope_hi(x0, x1, c, s));
   if (x != nullptr) {
     x[lane] = y0;
     x[lane + 64] = y1;

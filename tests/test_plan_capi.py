@@ -528,3 +528,43 @@ def test_attention_rejects_plan_for_another_block_table(lib):
     for rows, stride in ((1, 4096), (2, 2048)):
         assert _attention_with_plan(lib, words, bt_rows=rows, bt_stride=stride) == 1
         assert "block table" in _lib.last_error()
+
+
+@pytest.mark.skipif(Path("/dev/kfd").exists(),
+                    reason="passes host buffers as device pointers: only where no GPU can run it")
+def test_fused_attention_rejects_bad_rows_before_launch(lib):
+    """The fused prologue + attention entry point refuses, before any HIP
+    call: misaligned or badly strided q/k/v rows, one norm weight without the
+    other, bad split counts, positions past the RoPE tables, and a plan that
+    splits one sequence's rows over several verify groups."""
+    from nebulasd_amd import _lib
+    from nebulasd_amd.plan import plan_words
+
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    buf = np.zeros(1 << 16, np.uint8)
+    p = buf.ctypes.data + (-buf.ctypes.data) % 16  # 16-byte aligned stand-in pointer
+    ws = np.zeros(1 << 22, np.uint8)
+    wp = ws.ctypes.data + (-ws.ctypes.data) % 16
+    hq, hkv, qs, kvs = 32, 8, 48 * 128, 48 * 128
+    sid = [0] * 5 + [1] * 5
+    sl = [3000 + i for i in range(1, 6)] + [900 + i for i in range(1, 6)]
+    words, _ = plan_words(sid, sl, hq, hkv, 128, 16, 2, 4096, 32)
+
+    def call(q=p, k=p + 4096, v=p + 8192, ks=kvs, vs=kvs, part=None, splits=0, qn=p, kn=p, n_pos=4096,
+             plan=words):
+        return lib.nsd_paged_attention_fused(
+            q, qs, k, ks, v, vs, part, splits, qn, kn, 1e-6, p, p, n_pos, p, None, p, p, 1000, 2, 0, hq, hkv,
+            128, 16, p, 2, 4096, plan.ctypes.data_as(i32p), p, wp, ws.size - 16, 128 ** -0.5, None, None)
+
+    for kwargs, msg in (({"k": p + 4098}, "16-byte aligned"), ({"v": p + 8200 + 2}, "16-byte aligned"),
+                        ({"vs": kvs + 4}, "multiples of 8"), ({"ks": 1000}, "multiples of 8"),
+                        ({"kn": None}, "both norm weights"), ({"part": p, "splits": 17}, "splits=17"),
+                        ({"n_pos": 3004}, "outside the 3004-row RoPE tables")):
+        assert call(**kwargs) == 1, (kwargs, _lib.last_error())
+        assert msg in _lib.last_error(), (kwargs, _lib.last_error())
+    # 17 rows of one request at GQA 4 exceed one 48-row group: the plan splits it
+    split, _ = plan_words([0] * 17, [500 + i for i in range(1, 18)], hq, hkv, 128, 16, 1, 4096, 32,
+                          max_group_rows=48)
+    assert int(split[_lib.PLAN_GROUPS]) > 1
+    assert call(plan=split) == 2, _lib.last_error()  # NSD_ERR_UNSUPPORTED
+    assert "several verify groups" in _lib.last_error()
