@@ -9,8 +9,11 @@
  *
  *   fused_add_rmsnorm(x, residual, input_layernorm)            (:98-103)
  *   qkv = x . W_qkv^T  (the q/k/v projections stacked; one GEMM for :107-109)
- *   QK-RMSNorm + RoPE + KV store of the new rows, one launch     (:114-145)
+ *   QK-RMSNorm + RoPE + KV store of the new rows                (:114-145)
  *   o = paged_attention(q)                                       (:169-183)
+ *     (these two in one launch, nsd_paged_attention_fused, for decode
+ *     batches: a group's query rows per kv head within one 16-row tile and
+ *     every sequence in one group; else two launches)
  *   o = o . W_o^T                                                (:189)
  *   fused_add_rmsnorm(o, residual, post_attention_layernorm)     (:192)
  *   h = fp16(up) * fp16(silu(fp16(gate))) of o . W_up_gate^T     (:199-200)
@@ -19,8 +22,8 @@
  * on this library's kernels (nsd_attn.h), the q/k/v, O and down projections
  * included (nsd_linear_partials, whose split partials the next kernel sums
  * where it reads the projection), all enqueued on the caller's stream from
- * C++: the host cost of a layer is ten launches instead of a dozen Python
- * calls.  The embedding lookup before the stack and the final residual add
+ * C++: the host cost of a layer is its kernel launches instead of a dozen
+ * Python calls.  The embedding lookup before the stack and the final residual add
  * and post-layer after it stay with the caller.
  *
  * nsd_decoder_create allocates the executor's device buffers (activations
@@ -70,10 +73,12 @@ int nsd_decoder_destroy(nsd_decoder* dec);
  * 292).  residual [n_rows, hidden] must be zero on entry.  The caches,
  * block table, seq_ids / seq_lens (int32 device [n_rows]), cos/sin tables
  * and the attention plan and workspace are those of nsd_qk_norm_rope_store
- * and nsd_paged_attention for the same rows.  probe_layer >= 0 copies that
- * layer's attention input q and output o ([n_rows, Hq, d] each) to probe_q /
- * probe_o and writes its natural-log LSE [n_rows, Hq] to probe_lse (for
- * checks); -1 for none.  status: optional device int32 word (NSD_STATUS_*).
+ * and nsd_paged_attention for the same rows (the plan built from these
+ * seq_ids / seq_lens).  probe_layer >= 0 copies that layer's attention input
+ * q and output o ([n_rows, Hq, d] each) to probe_q / probe_o and writes its
+ * natural-log LSE [n_rows, Hq] to probe_lse (for checks); that layer runs
+ * the prologue and the attention as two launches (same results).  -1 for
+ * none.  status: optional device int32 word (NSD_STATUS_*).
  */
 int nsd_decoder_forward(nsd_decoder* dec, void* x, void* residual, int64_t n_rows,
                         void* k_cache, void* v_cache, int64_t num_blocks,

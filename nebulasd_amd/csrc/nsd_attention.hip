@@ -49,9 +49,7 @@
 // Layouts (reference swiftLLM/swiftllm/worker/kernels/paged_attn.py):
 //   k/v cache [N, L, Hkv, 16, 128] fp16, block (blk, layer, head) = 4 KB
 //   contiguous at ((blk*L + layer)*Hkv + head)*16*128 (:49-50, :70-71).
-#include <algorithm>
 #include <mutex>
-#include <vector>
 
 #include "nsd_device.h"
 
@@ -418,21 +416,26 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) h[kk] = *reinterpret_cast<const f16x8*>(src + 32 * kk + 8 * lg);
       } else {
-        const float* prow = fx.part + r * fx.part_rs + (int64_t)hd * D;
+        // the splits summed in split order, a split's eight loads together
+        const float* prow = fx.part + r * fx.part_rs + (int64_t)hd * D + 8 * lg;
+        f32x4 acc[8];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          f32x4 s0 = *reinterpret_cast<const f32x4*>(prow + 32 * kk + 8 * lg);
-          f32x4 s1 = *reinterpret_cast<const f32x4*>(prow + 32 * kk + 8 * lg + 4);
-          for (int s2 = 1; s2 < fx.splits; ++s2) {
-            s0 += *reinterpret_cast<const f32x4*>(prow + s2 * fx.split_stride + 32 * kk + 8 * lg);
-            s1 += *reinterpret_cast<const f32x4*>(prow + s2 * fx.split_stride + 32 * kk + 8 * lg + 4);
-          }
+        for (int c = 0; c < 8; ++c) acc[c] = *reinterpret_cast<const f32x4*>(prow + 32 * (c >> 1) + 4 * (c & 1));
+        for (int s2 = 1; s2 < fx.splits; ++s2) {
+          const float* ps = prow + (int64_t)s2 * fx.split_stride;
+          f32x4 add[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) add[c] = *reinterpret_cast<const f32x4*>(ps + 32 * (c >> 1) + 4 * (c & 1));
+#pragma unroll
+          for (int c = 0; c < 8; ++c) acc[c] += add[c];
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            h[kk][j] = f16_of(s0[j]);
-            h[kk][j + 4] = f16_of(s1[j]);
+            h[kk][j] = f16_of(acc[2 * kk][j]);
+            h[kk][j + 4] = f16_of(acc[2 * kk + 1][j]);
           }
-        }
       }
     }
   };
@@ -983,21 +986,16 @@ extern "C" int nsd_paged_attention_fused(const void* q, int64_t q_row_stride, co
     return fail(NSD_ERR_INVALID,
                 "paged_attention_fused: q/k/v rows (16-byte aligned, strides multiples of 8 covering the heads)");
   }
-  // every sequence's new rows in one group, so that no workgroup reads a new
-  // row another one writes in the same launch; every position in the tables
+  // every position in the tables; every sequence's new rows in one group
   const int n_groups = plan_host[kPlanGroups];
   const int32_t* grp = plan_host + plan_host[kPlanOffGroups];
-  std::vector<int32_t> sids;
-  sids.reserve(n_groups);
   for (int g = 0; g < n_groups; ++g) {
     const int32_t* gr = grp + 4 * g;
     if ((int64_t)gr[3] + gr[1] > n_positions)
       return fail(NSD_ERR_INVALID, "paged_attention_fused: position %lld outside the %lld-row RoPE tables",
                   (long long)gr[3] + gr[1] - 1, (long long)n_positions);
-    sids.push_back(gr[2]);
   }
-  std::sort(sids.begin(), sids.end());
-  if (std::adjacent_find(sids.begin(), sids.end()) != sids.end())
+  if (!plan_keeps_sequences_whole(plan_host))
     return fail(NSD_ERR_UNSUPPORTED,
                 "paged_attention_fused: a sequence's rows span several verify groups (run the prologue, then "
                 "paged_attention)");

@@ -79,6 +79,12 @@ constexpr int kMinPieceBlocks = 4;
 constexpr int kWavesPerPiece = 4;       // waves of an attention workgroup (wave w: blocks w, w + 4, ...)
 constexpr int kXcds = 8;                // workgroup i of a launch runs on XCD i % 8
 
+// Whether a plan keeps every sequence's rows in one verify group, as the
+// fused prologue + attention launch needs (then no workgroup reads a new K/V
+// row that another one writes in the same launch).  plan_host is a checked
+// plan's header and tables.
+bool plan_keeps_sequences_whole(const int32_t* plan_host);
+
 // Attention workspace: the claim counter of plans with claimed records
 // (zero between calls; its 256 bytes are reserved in every layout, so no
 // other plan's partials land there), then the partials of the split

@@ -3,10 +3,11 @@
 // nsd_decoder_forward enqueues, for every layer, the reference's layer body
 // (swiftLLM/swiftllm/worker/layers/transformer_layer.py:83-201) on the
 // caller's stream, all of it this library's kernels: fused add-RMSNorm, the
-// q/k/v projection, the QK-norm + RoPE + KV-store prologue, paged attention,
-// the O projection, fused add-RMSNorm, fused up/gate + SiLU-and-mul and the
-// down projection.  The layer loop runs in C++, so a layer costs the host
-// ten enqueues.
+// q/k/v projection, the QK-norm + RoPE + KV-store prologue and paged
+// attention (one launch, nsd_paged_attention_fused, for decode batches), the
+// O projection, fused add-RMSNorm,
+// fused up/gate + SiLU-and-mul and the down projection.  The layer loop runs
+// in C++, so a layer costs the host its kernel enqueues and nothing else.
 //
 // The q/k/v, O and down projections are nsd_linear_partials calls: each
 // writes fp32 split partials that the kernel after it sums where it reads
@@ -124,6 +125,16 @@ extern "C" int nsd_decoder_forward(nsd_decoder* dec, void* x, void* residual, in
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t H = dec->hidden, I = dec->inter, hq = dec->hq, hkv = dec->hkv, d = dec->d;
   const int64_t qkv_w = (hq + 2 * hkv) * d;
+  // The prologue runs inside the attention's launch (one launch instead of
+  // two, the same bits) where the plan keeps every sequence's rows in one
+  // verify group and a group's query rows per kv head fit one 16-row tile
+  // (decode batches).  Every wave of the attention builds its group's query
+  // rows from the q/k/v projection's split partials; past one tile that
+  // re-reading costs more than the prologue's own launch (at the Qwen3-8B
+  // verify batch, 16 x 5 rows and five splits, the stack's layer took 169 us
+  // with the fused launch against 157 us with two).  The probe layer keeps
+  // the two calls, whose q it copies out.
+  const bool fused = plan_host != nullptr && plan_host[kPlanRowsMax] <= 16 && plan_keeps_sequences_whole(plan_host);
   int rc = NSD_OK;
   for (int li = 0; li < dec->layers && rc == NSD_OK; ++li) {
     const nsd_decoder_layer& lw = dec->w[li];
@@ -133,12 +144,19 @@ extern "C" int nsd_decoder_forward(nsd_decoder* dec, void* x, void* residual, in
                  : nsd_fused_add_rmsnorm_partials(dec->part, dec->s_down, x, residual, lw.norm_in, n_rows, H,
                                                   dec->eps, stream);
     if (rc == NSD_OK) rc = nsd_linear_partials(x, lw.w_qkv, dec->part, n_rows, qkv_w, H, stream);
-    if (rc == NSD_OK)
+    const bool one_launch = fused && li != probe_layer;
+    if (rc == NSD_OK && one_launch)
+      rc = nsd_paged_attention_fused(nullptr, 0, nullptr, 0, nullptr, 0, dec->part, dec->s_qkv, lw.q_norm, lw.k_norm,
+                                     dec->eps, cos_cache, sin_cache, n_positions, dec->o, nullptr, k_cache, v_cache,
+                                     num_blocks, dec->layers, li, (int)hq, (int)hkv, (int)d, 16, block_table, bt_rows,
+                                     bt_stride, plan_host, plan_dev, attn_workspace, attn_workspace_bytes,
+                                     softmax_scale, status, stream);
+    if (rc == NSD_OK && !one_launch)
       rc = nsd_qk_norm_rope_store_partials(dec->part, dec->s_qkv, dec->q, lw.q_norm, lw.k_norm, dec->eps, cos_cache,
                                            sin_cache, n_positions, k_cache, v_cache, block_table, bt_rows, bt_stride,
                                            seq_ids, seq_lens, n_rows, num_blocks, dec->layers, li, (int)hq, (int)hkv,
                                            (int)d, 16, status, stream);
-    if (rc == NSD_OK)
+    if (rc == NSD_OK && !one_launch)
       rc = nsd_paged_attention(dec->q, dec->o, li == probe_layer ? probe_lse : nullptr, k_cache, v_cache, num_blocks,
                                dec->layers, li, (int)hq, (int)hkv, (int)d, 16, block_table, bt_rows, bt_stride,
                                plan_host, plan_dev, attn_workspace, attn_workspace_bytes, softmax_scale, status,

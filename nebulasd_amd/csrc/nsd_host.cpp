@@ -25,6 +25,15 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+bool plan_keeps_sequences_whole(const int32_t* plan_host) {
+  const int n_groups = plan_host[kPlanGroups];
+  const int32_t* grp = plan_host + plan_host[kPlanOffGroups];  // [n_groups][4] {row_start, q_len, seq_id, ctx}
+  std::vector<int32_t> sids(n_groups);
+  for (int g = 0; g < n_groups; ++g) sids[g] = grp[4 * g + 2];
+  std::sort(sids.begin(), sids.end());
+  return std::adjacent_find(sids.begin(), sids.end()) == sids.end();
+}
+
 }  // namespace nsd
 
 using namespace nsd;

@@ -7,7 +7,8 @@ target's decode/verify batches the GPU finishes a layer faster than Python
 issues it.  ``DecoderStack`` hands the whole stack of a forward to one C++
 call that enqueues the same sequence on the current stream: fused
 add-RMSNorm, one q/k/v projection, the fused QK-norm + RoPE + KV-store
-prologue, paged attention, the O projection, fused add-RMSNorm, the fused
+prologue and paged attention (one launch for decode batches), the O
+projection, fused add-RMSNorm, the fused
 up/gate + SiLU-and-mul, the down projection (the projections are this
 library's split-k GEMM, whose fp32 split partials the next kernel sums where
 it reads them).  The embedding lookup and the post-layer stay in Python.

@@ -173,3 +173,47 @@ def test_decoder_layer_matches_float64_oracle(gpu, cfg, n_req, depth):
     for sid, n in zip(sids, slens):
         mask[int(bt[sid, (n - 1) // 16]), :, (n - 1) % 16] = False
     assert np.array_equal(got_k[:, 0][mask], kc[:, 0][mask]) and np.array_equal(got_v[:, 0][mask], vc[:, 0][mask])
+
+
+@pytest.mark.parametrize("cfg,n_req,depth", [(QWEN3_8B, 16, 0), (QWEN3_0_6B, 64, 0), (QWEN3_0_6B, 16, 4)],
+                         ids=["8b-decode16", "0.6b-decode64", "0.6b-verify16x5"])
+def test_decoder_fused_layers_equal_two_launch_layers(gpu, cfg, n_req, depth):
+    """At batches whose groups fit one 16-row tile per kv head, a layer runs
+    its prologue inside the attention's launch unless it is the probe layer,
+    which runs them as two launches.  Two layers from the same state, with
+    no probe (both fused), a probe on layer 1 and a probe on layer 0: the
+    outputs, residuals and caches are the same bits."""
+    print(f"decoder fused vs two-launch layers: {n_req} requests, q_len {depth + 1}", flush=True)
+    cfg = dict(cfg, num_hidden_layers=2)
+    g = torch.Generator().manual_seed(11)
+    prompt_lens = torch.randint(20, 300, (n_req,), generator=g).tolist()
+    blocks = [(p + depth + 4) // 16 + 1 for p in prompt_lens]
+    m = RandomQwen3(cfg, blocks, gpu, seed=12, native=True)
+    prompts = [torch.randint(0, cfg["vocab_size"], (n,), generator=g).tolist() for n in prompt_lens]
+    m.prefill(list(range(n_req)), prompts)
+    sids, slens, toks = [], [], []
+    for r, p in enumerate(prompts):
+        rows = [p[-1]] + torch.randint(0, cfg["vocab_size"], (depth,), generator=g).tolist()
+        sids += [r] * len(rows)
+        slens += list(range(len(p) + 1, len(p) + 1 + len(rows)))
+        toks += rows
+    from nebulasd_amd.infer_state import build_infer_state
+
+    st = build_infer_state(sids, slens, [], m.mc, m.cos, m.sin, gpu)
+    x0 = m.embed[torch.tensor(toks, device=gpu)]
+    kc0, vc0 = m.k_cache.clone(), m.v_cache.clone()
+    stack = DecoderStack(m.mc, m.layers)
+    runs = []
+    for probe in (-1, 1, 0):
+        m.k_cache.copy_(kc0)
+        m.v_cache.copy_(vc0)
+        x, res = x0.clone(), torch.zeros_like(x0)
+        stack.forward(x, res, m.k_cache, m.v_cache, m.block_table, m.ec, st, m.cos, m.sin, probe_layer=probe)
+        torch.cuda.synchronize()
+        runs.append((x, res, m.k_cache.clone(), m.v_cache.clone()))
+    stack.close()
+    assert st.attn_plan.rows_max <= 16, "a batch the stack runs fused"
+    assert not torch.equal(runs[0][2], kc0), "the new K rows were written"
+    for probe, run in zip((1, 0), runs[1:]):
+        for a, b, what in zip(runs[0], run, ("output", "residual", "k cache", "v cache")):
+            assert torch.equal(a, b), (probe, what)
