@@ -540,23 +540,54 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *reinterpret_cast<const f16x8*>(qrow + 32 * kk + 8 * lg);
     }
-  } else {
-    // every load first (the new rows', the query rows'), then the arithmetic
+  } else if constexpr (NT == 1) {
+    // One row tile: every wave builds it (rows past the group read its row
+    // 0 and are never stored), its loads before its arithmetic; no barrier.
     const bool own_late = own && !own_early;
     if (own_late) load_new();
-    f16x8 qh[NT][4], qcs[NT][4], qw[4];
+    const int nr = lr < n_rows ? lr : 0;
+    const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
+    f16x8 qh[4], qcs[4], qw[4];
     load_w(fx.qn, qw);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int n = 16 * t + lr;
+    load_row(row_start + qi, head * a.gqa + gh, qh);
+    load_cs(ctx + qi, qcs);
+    if (own_late) store_new();
+    norm_rope(qh, fx.qn != nullptr, qw, qcs, qf[0]);
+  } else {
+    // Wave t < NT builds row tile t (rows past the group are zero and never
+    // stored) into the LDS after the buffers; after a barrier every wave
+    // reads all the tiles.  The wave's loads (the new rows', its tile's) go
+    // out before its arithmetic.
+    const bool own_late = own && !own_early;
+    if (own_late) load_new();
+    const bool builds = wave < NT;  // uniform over the wave
+    const int n = 16 * wave + lr;
+    f16x8 qh[4], qcs[4], qw[4];
+    if (builds) {
+      load_w(fx.qn, qw);
       const int nr = n < n_rows ? n : 0;
       const int qi = nr / a.gqa, gh = nr - qi * a.gqa;
-      load_row(row_start + qi, head * a.gqa + gh, qh[t]);
-      load_cs(ctx + qi, qcs[t]);
+      if (n < n_rows) {
+        load_row(row_start + qi, head * a.gqa + gh, qh);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) qh[kk] = f16x8{};
+      }
+      load_cs(ctx + qi, qcs);
     }
     if (own_late) store_new();
+    lds_char* qlds = lds_all + kLdsBytes;
+    if (builds) {
+      f16x8 qo[4];
+      norm_rope(qh, fx.qn != nullptr, qw, qcs, qo);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) norm_rope(qh[t], fx.qn != nullptr, qw, qcs[t], qf[t]);
+      for (int kk = 0; kk < 4; ++kk) *(lds_f16x8*)(qlds + ((wave * 4 + kk) * kWave + lane) * 16) = qo[kk];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) qf[t][kk] = *(const lds_f16x8*)(qlds + ((t * 4 + kk) * kWave + lane) * 16);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
@@ -709,10 +740,20 @@ int launch_nt(const AttnArgs& args, const PieceTable& pt, int grid, hipStream_t 
   return launch_status("paged_attention");
 }
 
+// The fused kernel's LDS: the buffers, then its query row tiles (4 KB each)
+// when it has more than one.
+template <int NT>
+constexpr int fused_lds_bytes() { return kLdsBytes + (NT > 1 ? NT * 16 * D * 2 : 0); }
+static_assert(2 * fused_lds_bytes<3>() <= 160 * 1024, "two fused workgroups per CU");
+
 template <int NT>
 int launch_nt_fused(const AttnArgs& args, const PieceTable& pt, const FusedArgs& f, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_attn_kernel<NT, FusedArgs>), dim3(grid), dim3(kThreads), kLdsBytes, stream, args, pt,
-                     f);
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_attn_kernel<NT, FusedArgs>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, fused_lds_bytes<NT>());
+  if (attr != hipSuccess)
+    return fail(NSD_ERR_HIP, "paged_attention_fused: LDS attribute: %s", hipGetErrorString(attr));
+  hipLaunchKernelGGL((paged_attn_kernel<NT, FusedArgs>), dim3(grid), dim3(kThreads), fused_lds_bytes<NT>(), stream,
+                     args, pt, f);
   return launch_status("paged_attention_fused");
 }
 

@@ -128,12 +128,12 @@ extern "C" int nsd_decoder_forward(nsd_decoder* dec, void* x, void* residual, in
   // The prologue runs inside the attention's launch (one launch instead of
   // two, the same bits) where the plan keeps every sequence's rows in one
   // verify group and a group's query rows per kv head fit one 16-row tile
-  // (decode batches).  Every wave of the attention builds its group's query
-  // rows from the q/k/v projection's split partials; past one tile that
-  // re-reading costs more than the prologue's own launch (at the Qwen3-8B
-  // verify batch, 16 x 5 rows and five splits, the stack's layer took 169 us
-  // with the fused launch against 157 us with two).  The probe layer keeps
-  // the two calls, whose q it copies out.
+  // (decode batches: the Qwen3-0.6B draft layer 91.5 us against 93.8 us).
+  // Past one tile every piece builds its group's query rows from the q/k/v
+  // projection's five split partials, which gains nothing over the
+  // prologue's own launch (the Qwen3-8B verify layer, 16 x 5 rows: 154.9 us
+  // fused against 155.0 us), so verify batches keep two launches.  The
+  // probe layer keeps the two calls, whose q it copies out.
   const bool fused = plan_host != nullptr && plan_host[kPlanRowsMax] <= 16 && plan_keeps_sequences_whole(plan_host);
   int rc = NSD_OK;
   for (int li = 0; li < dec->layers && rc == NSD_OK; ++li) {
