@@ -60,8 +60,11 @@ def _outputs(w, mc):
 
 @pytest.mark.parametrize("model,q_len,claims", [
     (QWEN3_8B, 5, False), (QWEN3_8B, 1, False), (QWEN3_8B, 9, False), (QWEN3_0_6B, 1, False),
-    (QWEN3_0_6B, 5, False), (QWEN3_8B, 1, True), (QWEN3_8B, 12, False)],
-    ids=["8b-q5", "8b-q1", "8b-q9", "06b-q1", "06b-q5", "8b-q1-claimed", "8b-q12"])
+    (QWEN3_0_6B, 5, False), (QWEN3_8B, 1, True), (QWEN3_8B, 12, False),
+    (dict(QWEN3_8B, num_attention_heads=40), 5, False), (dict(QWEN3_8B, num_attention_heads=64), 5, False),
+    (dict(QWEN3_8B, num_attention_heads=8), 16, False), (dict(QWEN3_8B, num_key_value_heads=4), 1, False)],
+    ids=["8b-q5", "8b-q1", "8b-q9", "06b-q1", "06b-q5", "8b-q1-claimed", "8b-q12", "gqa5-q5", "gqa8-q5",
+         "gqa1-q16", "32x4-q1"])
 def test_fused_equals_prologue_then_attention(gpu, model, q_len, claims, monkeypatch):
     print(f"fused vs unfused, q_len {q_len}, claims {claims}", flush=True)
     if claims:
@@ -174,3 +177,30 @@ def test_fused_matches_oracle(gpu):
         new[blk, layer, :, (n - 1) % 16, :] = True
     assert not (diff & ~new).any(), "only the new K rows may differ from the oracle's pool"
     np.testing.assert_allclose(kg[new].astype(np.float64), kc_h[new].astype(np.float64), atol=1e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("col", [2, 5], ids=["mid-context", "new-rows"])
+def test_fused_bad_block_is_flagged(gpu, col):
+    """An out-of-range block id, inside a sequence's context or where its new
+    rows go, is skipped and reported, not faulted on: the fused launch gives
+    the two calls' o, lse and pools (both skip the block) and its status word
+    names the bad block."""
+    print(f"fused, bad block id at column {col}", flush=True)
+    w, mc, ec, st, cos, sin, k, v, qn, kn = _setup(gpu, QWEN3_8B, 5, seed=71, ctxs=[40, 90])
+    w.block_table[1, col] = w.k_cache.shape[0] + 5  # ctx 90: new rows at 90..94, block 5
+    layer = 1
+    kc0, vc0 = w.k_cache.clone(), w.v_cache.clone()
+    qa = w.q.clone()
+    qk_norm_rope_store(qa, k.clone(), v, w.k_cache, w.v_cache, w.block_table, qn, kn, mc, ec, st, layer, cos, sin)
+    oa, la = _outputs(w, mc)
+    paged_attention(qa, w.k_cache, w.v_cache, w.block_table, mc, ec, st, layer, oa, la)
+    torch.cuda.synchronize()
+    kca, vca = w.k_cache.clone(), w.v_cache.clone()
+    w.k_cache.copy_(kc0)
+    w.v_cache.copy_(vc0)
+    ob, lb = _outputs(w, mc)
+    with pytest.raises(RuntimeError, match="block id outside the pool"):
+        paged_attention_fused(w.q, k, v, w.k_cache, w.v_cache, w.block_table, qn, kn, mc, ec, st, layer, cos, sin,
+                              ob, lb, validate=True)
+    assert torch.equal(ob, oa) and torch.equal(lb, la)
+    assert torch.equal(w.k_cache, kca) and torch.equal(w.v_cache, vca)
