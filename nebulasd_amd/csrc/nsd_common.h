@@ -75,7 +75,10 @@ constexpr int kBlockTokens = 16;
 constexpr int kMaxGroupRows = 48;       // query rows of one segment: three 16-row tiles in one wave
 constexpr int kMaxSlotsPerSegment = 128;
 constexpr int kMaxPieceBlocks = 256;    // blocks of one piece (four waves, one block id per lane)
-constexpr int kMinPieceBlocks = 4;
+// Shortest piece a cut makes: two blocks per wave, whose loads are both in
+// flight from the piece's start, so a shorter cut saves no latency and only
+// adds the merge of the segment's pieces.
+constexpr int kMinPieceBlocks = 8;
 constexpr int kWavesPerPiece = 4;       // waves of an attention workgroup (wave w: blocks w, w + 4, ...)
 constexpr int kXcds = 8;                // workgroup i of a launch runs on XCD i % 8
 

@@ -210,7 +210,7 @@ def test_attention_graph_replay_bit_identical(gpu, q_len, monkeypatch):
     if q_len != 5:
         monkeypatch.setattr(planmod, "PIECES_PER_SLOT", 2.0)
     w = make_workload("target_verify", 9, device=gpu, pool_blocks=4096, num_layers=3,
-                      ctxs=[3000, 40, 1500, 700, 9], q_len=q_len)
+                      ctxs=[6000, 40, 3000, 1400, 9], q_len=q_len)
     mc = ModelConfig(w.spec.model)
     ec = EngineConfig(block_size=16, max_blocks_per_seq=w.block_table.shape[1])
     cos, sin = rope_cache(mc.head_dim, mc.rope_theta, max(w.seq_lens) + 1, w.q.device)

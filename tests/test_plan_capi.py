@@ -69,7 +69,7 @@ def test_error_paths_without_gpu(lib):
 
 
 # planner constants (nebulasd_amd/csrc/nsd_common.h)
-MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, MAX_SLOTS, XCDS, MAX_GROUP_ROWS = 256, 4, 128, 8, 48
+MAX_PIECE_BLOCKS, MIN_PIECE_BLOCKS, MAX_SLOTS, XCDS, MAX_GROUP_ROWS = 256, 8, 128, 8, 48
 
 
 def _plan(seq_ids, seq_lens, hq=32, hkv=8, workers=64, max_group_rows=0, bt_rows=None, stride=4096,
