@@ -204,3 +204,43 @@ def test_fused_bad_block_is_flagged(gpu, col):
                               ob, lb, validate=True)
     assert torch.equal(ob, oa) and torch.equal(lb, la)
     assert torch.equal(w.k_cache, kca) and torch.equal(w.v_cache, vca)
+
+
+@pytest.mark.parametrize("q_len", [5, 1], ids=["verify", "decode"])
+def test_fused_graph_replay_bit_identical(gpu, q_len):
+    """A HIP graph of fused launches over every layer replays to the eager
+    results bit for bit, replay after replay, with eager calls in between:
+    o, lse and both pools (the new rows written again to the same slots)."""
+    print(f"fused graph replay, q_len {q_len}", flush=True)
+    w, mc, ec, st, cos, sin, k, v, qn, kn = _setup(gpu, QWEN3_8B, q_len, seed=81)
+    layers = w.k_cache.shape[1]
+    outs = [_outputs(w, mc) for _ in range(layers)]
+
+    def calls():
+        for layer in range(layers):
+            paged_attention_fused(w.q, k, v, w.k_cache, w.v_cache, w.block_table, qn, kn, mc, ec, st, layer, cos,
+                                  sin, outs[layer][0], outs[layer][1])
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [(o.clone(), l.clone()) for o, l in outs]
+    kc, vc = w.k_cache.clone(), w.v_cache.clone()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            calls()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o, l in outs:
+            o.zero_()
+            l.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(layers):
+            assert torch.equal(outs[layer][0], eager[layer][0]), f"replay {rep} layer {layer} o"
+            assert torch.equal(outs[layer][1], eager[layer][1]), f"replay {rep} layer {layer} lse"
+        assert torch.equal(w.k_cache, kc) and torch.equal(w.v_cache, vc), f"replay {rep} pools"
+        calls()  # eager work between replays
+        torch.cuda.synchronize()
