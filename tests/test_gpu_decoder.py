@@ -217,3 +217,66 @@ def test_decoder_fused_layers_equal_two_launch_layers(gpu, cfg, n_req, depth):
     for probe, run in zip((1, 0), runs[1:]):
         for a, b, what in zip(runs[0], run, ("output", "residual", "k cache", "v cache")):
             assert torch.equal(a, b), (probe, what)
+
+
+@pytest.mark.parametrize("cfg,n_req,depth", [(QWEN3_0_6B, 64, 0), (QWEN3_8B, 16, 4)],
+                         ids=["0.6b-decode64", "8b-verify16x5"])
+def test_decoder_stack_graph_replay_bit_identical(gpu, cfg, n_req, depth):
+    """The stack's forward captured in a HIP graph replays to the eager
+    forward bit for bit (output, residual, caches), three replays from the
+    same inputs, with an eager forward between them: the decode batch runs
+    the prologue inside the attention launch, the verify batch as two."""
+    print(f"decoder stack graph replay: {n_req} requests, q_len {depth + 1}", flush=True)
+    cfg = dict(cfg, num_hidden_layers=2)
+    g = torch.Generator().manual_seed(21)
+    prompt_lens = torch.randint(20, 300, (n_req,), generator=g).tolist()
+    blocks = [(p + depth + 4) // 16 + 1 for p in prompt_lens]
+    m = RandomQwen3(cfg, blocks, gpu, seed=22, native=True)
+    prompts = [torch.randint(0, cfg["vocab_size"], (n,), generator=g).tolist() for n in prompt_lens]
+    m.prefill(list(range(n_req)), prompts)
+    sids, slens, toks = [], [], []
+    for r, p in enumerate(prompts):
+        rows = [p[-1]] + torch.randint(0, cfg["vocab_size"], (depth,), generator=g).tolist()
+        sids += [r] * len(rows)
+        slens += list(range(len(p) + 1, len(p) + 1 + len(rows)))
+        toks += rows
+    from nebulasd_amd.infer_state import build_infer_state
+
+    st = build_infer_state(sids, slens, [], m.mc, m.cos, m.sin, gpu)
+    x0 = m.embed[torch.tensor(toks, device=gpu)]
+    kc0, vc0 = m.k_cache.clone(), m.v_cache.clone()
+    x, res = x0.clone(), torch.zeros_like(x0)
+    stack = DecoderStack(m.mc, m.layers)
+
+    def reset():
+        x.copy_(x0)
+        res.zero_()
+        m.k_cache.copy_(kc0)
+        m.v_cache.copy_(vc0)
+
+    def fwd():
+        stack.forward(x, res, m.k_cache, m.v_cache, m.block_table, m.ec, st, m.cos, m.sin)
+
+    fwd()
+    torch.cuda.synchronize()
+    want = (x.clone(), res.clone(), m.k_cache.clone(), m.v_cache.clone())
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    reset()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            fwd()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        reset()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, exp, what in zip((x, res, m.k_cache, m.v_cache), want, ("output", "residual", "k cache", "v cache")):
+            assert torch.equal(got, exp), (rep, what)
+        reset()
+        fwd()  # eager work between replays
+        torch.cuda.synchronize()
+    del graph
+    stack.close()
