@@ -242,3 +242,35 @@ def test_post_layer_forward_matches_oracle(gpu):
     assert got.shape == (st.batch_size,)
     assert (got == want).mean() >= 0.8 and all(
         abs(float(logits[i, got[i]]) - float(logits[i, want[i]])) <= 2e-2 for i in range(len(got)))
+
+
+def test_lm_head_argmax_graph_replay(gpu):
+    """Replays of a captured pair of lm_head + argmax calls give the eager
+    tokens every time: each call's finalize leaves the key buffer at zero for
+    the next call, replayed or eager (Qwen3-0.6B shape, 64 rows)."""
+    g = torch.Generator(device=gpu).manual_seed(3)
+    w = (torch.randn(151936, 1024, device=gpu, generator=g) * 0.05).half()
+    xs = [torch.randn(64, 1024, device=gpu, generator=g).half() for _ in range(2)]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        want = [lm_head_argmax(x, w) for x in xs]  # eager on the capture stream first
+    torch.cuda.synchronize()
+    assert not torch.equal(want[0], want[1])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            got = [lm_head_argmax(x, w) for x in xs]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for t in got:
+            t.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), rep
+        with torch.cuda.stream(stream):
+            again = [lm_head_argmax(x, w) for x in xs]  # eager calls between replays
+        torch.cuda.synchronize()
+        for a, b in zip(again, want):
+            assert torch.equal(a, b), rep
