@@ -157,3 +157,41 @@ def test_prefill_prompt_order_is_only_a_schedule(gpu):
               w.k.shape[1], 128, 128 ** -0.5, status.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert status.item() & _lib.STATUS_BAD_SEQ
+
+
+def test_prefill_graph_replay_bit_identical(gpu):
+    """A HIP graph of prefill calls replays to the eager output and LSE bit
+    for bit, three times, with eager calls between (the prompts' longest-first
+    order is computed by the eager call before capture and reused)."""
+    w = make_prefill_workload("prefill_target", 8, device=gpu, lens=[40, 700, 5, 300, 1000, 64])
+    mx = max(w.lens)
+    lses = [torch.empty(w.q.shape[:2], dtype=torch.float32, device=gpu) for _ in range(2)]
+    stream = torch.cuda.Stream()
+
+    def calls():
+        return [flash_attn_varlen_func(w.q, w.k, w.v, w.cu_seqlens, w.cu_seqlens, mx, mx,
+                                       softmax_scale=w.spec.head_dim ** -0.5, causal=True, lse=lse)
+                for lse in lses]
+
+    with torch.cuda.stream(stream):
+        want = [(o, lse.clone()) for o, lse in zip(calls(), lses)]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            got = calls()  # outputs in the graph's memory, rewritten by every replay
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o, lse in zip(got, lses):
+            o.zero_()
+            lse.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, lse, (wo, wl) in zip(got, lses, want):
+            assert torch.equal(o, wo) and torch.equal(lse, wl), rep
+        with torch.cuda.stream(stream):
+            again = calls()
+        torch.cuda.synchronize()
+        for o, (wo, _) in zip(again, want):
+            assert torch.equal(o, wo), rep
