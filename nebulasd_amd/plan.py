@@ -149,6 +149,15 @@ class AttnPlan:
     def n_rows(self) -> int:
         return int(self.host[_lib.PLAN_ROWS])
 
+    @property
+    def keeps_sequences_whole(self) -> bool:
+        """Whether every sequence's rows sit in one verify group, as the
+        prologue inside the attention launch (``paged_attention_fused``) needs."""
+        h = self.host
+        n, og = int(h[_lib.PLAN_GROUPS]), int(h[_lib.PLAN_OFF_GROUPS])
+        sids = h[og:og + 4 * n].reshape(n, 4)[:, 2]
+        return len(np.unique(sids)) == n
+
     def fits(self, num_q_heads: int, num_kv_heads: int, block_table) -> bool:
         """Whether this plan serves calls with these head counts and block table
         (the table has the row stride the plan was built for and at least its rows)."""

@@ -4,8 +4,10 @@ This drives the attention path the way NebulaSD's swiftLLM backend does, at
 real model shapes, so that every layer call of a speculative run goes through
 this package's gfx950 kernels:
 
-* decode / verify rows: QK-RMSNorm + RoPE + KV store in one launch
-  (``qk_norm_rope_store``), then paged attention, in the order of
+* decode / verify rows: QK-RMSNorm + RoPE + KV store and paged attention in
+  one launch (``paged_attention_fused``), or, on a sampled-check layer or
+  with the forward-phase ranges on, the prologue in one launch
+  (``qk_norm_rope_store``) then paged attention, in the order of
   swiftLLM/swiftllm/worker/layers/transformer_layer.py:105-185;
 * prefill: ``rmsnorm_inplace`` on q/k, ``rotary_embedding_inplace``, the
   prefill ``store_kvcache`` and the prompts' causal attention in one launch
@@ -53,11 +55,12 @@ import torch.nn.functional as F
 from .config import QWEN3_0_6B, QWEN3_8B, EngineConfig, ModelConfig
 from .infer_state import build_infer_state, host_to_device, model_rope_cache
 from .kernels import (FUSED_UP_GATE_MAX_ROWS, flash_attn_varlen_func, fused_add_rmsnorm_inplace, paged_attention,
-                      post_layer_forward, qk_norm_rope_store, rmsnorm_inplace, rotary_embedding_inplace,
-                      silu_and_mul_inplace, store_kvcache, up_gate_silu_and_mul)
+                      paged_attention_fused, post_layer_forward, qk_norm_rope_store, rmsnorm_inplace,
+                      rotary_embedding_inplace, silu_and_mul_inplace, store_kvcache, up_gate_silu_and_mul)
 from .decoder import MAX_ROWS as DECODER_MAX_ROWS
 from .decoder import DecoderStack
 from .phases import ENABLED as PHASE_RANGES
+from .plan import plan_for
 from .phases import forward_phase_range
 from .speculative import compute_greedy_acceptance
 
@@ -190,6 +193,13 @@ class RandomQwen3:
         hq = mc.num_q_heads
 
         def attention(li, lw, q_rows, k, v):
+            checked = self.check is not None and self.check[0] == li
+            if not checked and not PHASE_RANGES and plan_for(st, mc, self.ec, self.block_table).keeps_sequences_whole:
+                # the prologue inside the attention's launch: the two calls' results, one launch
+                o = torch.empty(q_rows.shape, dtype=q_rows.dtype, device=dev)
+                paged_attention_fused(q_rows, k, v, self.k_cache, self.v_cache, self.block_table, lw["q_norm"],
+                                      lw["k_norm"], mc, self.ec, st, li, self.cos, self.sin, o)
+                return o
             q = torch.empty(q_rows.shape, dtype=q_rows.dtype, device=dev)  # the prologue's contiguous q
             with forward_phase_range(f"layer_{li}_store_kvcache"):  # QK-norm + RoPE + store, one launch
                 qk_norm_rope_store(q_rows, k, v, self.k_cache, self.v_cache, self.block_table,
