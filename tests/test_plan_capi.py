@@ -568,3 +568,22 @@ def test_fused_attention_rejects_bad_rows_before_launch(lib):
     assert int(split[_lib.PLAN_GROUPS]) > 1
     assert call(plan=split) == 2, _lib.last_error()  # NSD_ERR_UNSUPPORTED
     assert "several verify groups" in _lib.last_error()
+
+
+def test_plan_reports_whole_sequences(lib):
+    """AttnPlan.keeps_sequences_whole: true when every sequence's rows sit in
+    one verify group (what the fused prologue + attention launch needs),
+    false for a request whose 17 rows at GQA 4 (68 rows) the planner splits
+    over 48-row groups; it agrees with the native entry point's own check."""
+    from nebulasd_amd.plan import AttnPlan, plan_words
+
+    def plan(sids, slens, max_group_rows=0):
+        words, ws = plan_words(sids, slens, 32, 8, 128, 16, 4, 4096, 32, max_group_rows=max_group_rows)
+        return AttnPlan(host=words, dev=None, workspace=None, workspace_bytes=ws, num_q_heads=32, num_kv_heads=8)
+
+    whole = plan([0] * 5 + [1] * 5 + [3], [300 + i for i in range(1, 6)] + [900 + i for i in range(1, 6)] + [50])
+    assert whole.keeps_sequences_whole
+    split = plan([2] * 17, [500 + i for i in range(1, 18)], max_group_rows=48)
+    from nebulasd_amd import _lib
+
+    assert int(split.host[_lib.PLAN_GROUPS]) > 1 and not split.keeps_sequences_whole
