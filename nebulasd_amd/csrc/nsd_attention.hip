@@ -369,6 +369,17 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) dma_load(slot + kTile + c * 1024, vb + vsrc[c]);
   };
+  // one half of block jj's slot: its K tile (v = false) or its V tile
+  auto issue_half = [&](int jj, bool v) __attribute__((always_inline)) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)boff, jj);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)boff >> 32), jj);
+    const int64_t off = (int64_t)(((uint64_t)hi << 32) | lo);
+    const f16* b = (v ? a.v_cache : a.k_cache) + off;
+    const uint32_t dst = lds_base + (jj & 1) * kSlot + (v ? kTile : 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this half's earlier reads are done
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dma_load(dst + c * 1024, b + (v ? vsrc[c] : ksrc[c]));
+  };
 
   // The first two blocks' loads go out before the query rows', so the rows
   // arrive under the blocks' latency; then everything issued so far has
@@ -614,9 +625,22 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
     for (int mt = 0; mt < 8; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // One row tile: a block's K and V tiles are waited for and refilled
+  // separately (the next-but-one block's K goes out once this block's
+  // scores are read, its V once the PV product is); more tiles: a whole
+  // block at a time.
+  constexpr bool kHalves = NT == 1;
   for (int jj = 0; jj < my_n; ++jj) {
-    if (jj > 0) {  // blocks 0 and 1 are in; block jj + 1 goes into the slot block jj - 1 freed
-      if (jj + 1 < my_n) {
+    const bool more1 = jj + 1 < my_n, more2 = jj + 2 < my_n;
+    if constexpr (kHalves) {
+      // blocks 0 and 1 landed before the loop; for a later block, its K tile
+      // is in once at most V(jj), K(jj+1), V(jj+1) are outstanding
+      if (jj > 1) {
+        if (more1) wait_vm<12>();
+        else wait_vm<4>();
+      }
+    } else if (jj > 0) {  // blocks 0 and 1 are in; block jj + 1 goes into the slot block jj - 1 freed
+      if (more1) {
         issue(jj + 1);
         wait_vm<8>();  // this block landed; the next stays in flight
       } else {
@@ -635,6 +659,7 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) s[t] = mfma_k32(kop, qf[t][kk], s[t]);
     }
+    if (kHalves && more2) issue_half(jj + 2, false);  // block jj's K tile is read
     const int tok0 = blk * BS + 4 * lg;  // this lane's first token
     const bool masked = (bad_mask >> jj) & 1;
     const bool edge = masked || (blk + 1) * BS > ctx + 1;  // a token may lie past a row's length
@@ -668,12 +693,19 @@ void paged_attn_kernel(AttnArgs a, PieceTable pt, Extra fx) {
       }
       l[t] += psum;
     }
+    // V(jj) is in once at most K(jj+1), V(jj+1) and K(jj+2) are outstanding
+    if (kHalves && jj > 1) {
+      if (more2) wait_vm<12>();
+      else if (more1) wait_vm<8>();
+      else wait_vm<0>();
+    }
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const f16x4 va = ds_read_tr16(sl + vaddr0 + (((2 * mt + vc) ^ vsw) << 4));
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[t][mt] = mfma_k16(va, pb[t], acc[t][mt]);
     }
+    if (kHalves && more2) issue_half(jj + 2, true);  // block jj's V tile is read
   }
 
   // Merge the four waves' states, one row tile at a time, through the
