@@ -244,3 +244,20 @@ def test_fused_graph_replay_bit_identical(gpu, q_len):
         assert torch.equal(w.k_cache, kc) and torch.equal(w.v_cache, vc), f"replay {rep} pools"
         calls()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_fused_no_rows(gpu):
+    """A forward with no decode rows returns without a launch and writes nothing."""
+    mc = ModelConfig(QWEN3_8B)
+    ec = EngineConfig(max_blocks_per_seq=4)
+    cos, sin = rope_cache(128, 1e6, 8, gpu)
+    st = build_infer_state([], [], [], mc, cos, sin, gpu)
+    kc = torch.zeros((4, 1, 8, 16, 128), dtype=torch.float16, device=gpu)
+    vc = torch.zeros_like(kc)
+    q = torch.empty((0, 32, 128), dtype=torch.float16, device=gpu)
+    kv = torch.empty((0, 8, 128), dtype=torch.float16, device=gpu)
+    w = torch.ones(128, dtype=torch.float16, device=gpu)
+    paged_attention_fused(q, kv, kv, kc, vc, torch.zeros((1, 4), dtype=torch.int32, device=gpu), w, w, mc, ec, st,
+                          0, cos, sin, torch.empty_like(q))
+    torch.cuda.synchronize()
+    assert not kc.any() and not vc.any()
