@@ -252,6 +252,7 @@ def test_lm_head_argmax_graph_replay(gpu):
     w = (torch.randn(151936, 1024, device=gpu, generator=g) * 0.05).half()
     xs = [torch.randn(64, 1024, device=gpu, generator=g).half() for _ in range(2)]
     stream = torch.cuda.Stream()
+    torch.cuda.synchronize()  # w and x are written on the default stream
     with torch.cuda.stream(stream):
         want = [lm_head_argmax(x, w) for x in xs]  # eager on the capture stream first
     torch.cuda.synchronize()

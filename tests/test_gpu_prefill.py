@@ -173,6 +173,7 @@ def test_prefill_graph_replay_bit_identical(gpu):
                                        softmax_scale=w.spec.head_dim ** -0.5, causal=True, lse=lse)
                 for lse in lses]
 
+    torch.cuda.synchronize()  # the workload is written on the default stream
     with torch.cuda.stream(stream):
         want = [(o, lse.clone()) for o, lse in zip(calls(), lses)]
     torch.cuda.synchronize()
